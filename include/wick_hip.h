@@ -1,0 +1,95 @@
+/*
+ * wick_hip.h -- C ABI of the MI355X attention path for wick.
+ *
+ * Replaces, behind a C boundary that a Rust `extern "C"` module can bind with
+ * no new crates:
+ *   - KvCache (/root/reference/src/model.rs:251-275), its allocation
+ *     KvCache::new (:261-270) and per-layer slicing state_cache_layer (:556-559):
+ *     the cache becomes device-resident, laid out [layer][kv_head][pos][head_dim].
+ *   - the KV append in Model::forward (/root/reference/src/model.rs:481-483).
+ *   - Model::attention (/root/reference/src/model.rs:518-553), called once per
+ *     layer from Model::forward (/root/reference/src/model.rs:485).
+ *
+ * Conventions
+ *   - Every function returning int returns WICK_HIP_OK (0) or a negative
+ *     WICK_HIP_E* code; wick_hip_last_error() then describes the failure for
+ *     the calling thread.  Nothing aborts or throws across this boundary.
+ *   - Host pointers are borrowed for the duration of the call only.
+ *   - A handle owns its device memory and one HIP stream.  Calls on one handle
+ *     must be serialised by the caller (wick serialises sequences behind a
+ *     Mutex<Session>, /root/reference/src/server.rs:143,180).
+ *   - There is no CPU fallback: without a usable gfx950 device every call
+ *     fails with WICK_HIP_EDEVICE.
+ */
+#ifndef WICK_HIP_H
+#define WICK_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WICK_HIP_OK 0
+#define WICK_HIP_EINVAL (-1)  /* bad argument or shape                          */
+#define WICK_HIP_EHIP (-2)    /* a HIP runtime call failed                      */
+#define WICK_HIP_ENOMEM (-3)  /* device allocation failed                       */
+#define WICK_HIP_EDEVICE (-4) /* no usable GPU                                  */
+
+typedef struct wick_hip_kv wick_hip_kv;
+
+/* KvCache::new (src/model.rs:261-270): K and V for `layers` layers of
+ * `capacity` positions, zero-filled, on the current HIP device.
+ * head_dim must be 16, 32, 64 or 128. */
+int wick_hip_kv_create(int layers, int capacity, int kv_heads, int head_dim, wick_hip_kv **out);
+
+/* Drop of KvCache / State (src/model.rs:294-302).  NULL is a no-op. */
+void wick_hip_kv_destroy(wick_hip_kv *kv);
+
+/* The cache append of Model::forward (src/model.rs:481-483): rows k, v are
+ * host arrays [t][kv_heads*head_dim] for positions start..start+t of `layer`.
+ * Bit-exact copy.  Synchronous. */
+int wick_hip_kv_append(wick_hip_kv *kv, int layer, int start, int t, const float *k, const float *v);
+
+/* Read back positions pos0..pos0+n of `layer` in wick's host layout
+ * [n][kv_heads*head_dim] (either pointer may be NULL).  Synchronous. */
+int wick_hip_kv_read(const wick_hip_kv *kv, int layer, int pos0, int n, float *k, float *v);
+
+/* Model::attention (src/model.rs:518-553) for `layer`: q and att are host
+ * arrays [t][heads*head_dim]; token i attends to positions 0..=start+i, which
+ * must already be in the cache.  heads must be a multiple of kv_heads.
+ * att is fully overwritten.  Synchronous: att is valid on return. */
+int wick_hip_attention(wick_hip_kv *kv, int layer, int heads, const float *q, int t, int start, float *att);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *wick_hip_last_error(void);
+
+/* ---- device-resident variants (no counterpart in the reference: they let a
+ *      caller whose q / k / v / att already live in HBM skip the host copies).
+ *      Asynchronous on the handle's stream. */
+
+/* As wick_hip_kv_append, with k_dev / v_dev device arrays [t][kv_heads*head_dim]. */
+int wick_hip_kv_append_device(wick_hip_kv *kv, int layer, int start, int t, const float *k_dev, const float *v_dev);
+
+/* As wick_hip_attention, with q_dev / att_dev device arrays [t][heads*head_dim]. */
+int wick_hip_attention_device(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int t, int start,
+                              float *att_dev);
+
+/* Make the handle launch on `stream` (a hipStream_t; NULL = the handle's own). */
+int wick_hip_kv_set_stream(wick_hip_kv *kv, void *stream);
+
+/* Wait for all work queued on the handle's stream. */
+int wick_hip_kv_synchronize(wick_hip_kv *kv);
+
+/* Tuning knobs. */
+#define WICK_HIP_OPT_DECODE_CHUNK 1 /* positions per decode workgroup (multiple of 64; 0 = automatic) */
+#define WICK_HIP_OPT_PREFILL_PAIRING 2 /* 1 = pair causal row blocks (b, n-1-b); 0 = never; -1 = automatic */
+int wick_hip_kv_set_option(wick_hip_kv *kv, int option, int value);
+
+/* Number of workgroups the last attention call launched (for measurement). */
+int wick_hip_kv_last_grid(const wick_hip_kv *kv);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,57 @@
+"""The C ABI library loads and exports every symbol include/wick_hip.h declares.
+
+CPU-only: argument checks that fail before any device work are exercised; no
+compute call is made without a GPU.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+from wick_amd import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    with open(os.path.join(ROOT, "include", "wick_hip.h")) as f:
+        text = f.read()
+    return set(re.findall(r"\b(wick_hip_\w+)\s*\(", text))
+
+
+def test_header_and_binding_agree():
+    assert header_symbols() == set(_native.SIGNATURES)
+
+
+def test_library_exports_every_symbol():
+    lib = _native.load()
+    for name in header_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_argument_errors_without_device_work():
+    lib = _native.load()
+    h = ctypes.c_void_p()
+    assert lib.wick_hip_kv_create(1, 16, 2, 48, ctypes.byref(h)) == _native.EINVAL
+    assert b"head_dim" in lib.wick_hip_last_error()
+    assert lib.wick_hip_kv_create(0, 16, 2, 64, ctypes.byref(h)) == _native.EINVAL
+    assert lib.wick_hip_kv_create(1, 16, 2, 64, None) == _native.EINVAL
+    lib.wick_hip_kv_destroy(None)
+    assert lib.wick_hip_kv_set_option(None, 1, 64) == _native.EINVAL
+    assert lib.wick_hip_attention(None, 0, 4, None, 1, 0, None) == _native.EINVAL
+    assert lib.wick_hip_kv_last_grid(None) == 0
+
+
+def test_no_device_is_an_error_not_a_fallback():
+    try:
+        import torch
+        if torch.cuda.device_count() > 0:
+            pytest.skip("a GPU is present")
+    except ImportError:
+        pass
+    lib = _native.load()
+    h = ctypes.c_void_p()
+    rc = lib.wick_hip_kv_create(1, 16, 2, 64, ctypes.byref(h))
+    assert rc == _native.EDEVICE, rc
+    assert not h.value

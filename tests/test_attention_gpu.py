@@ -1,0 +1,187 @@
+"""Parity of the HIP attention path (through the C ABI) with the CPU oracle.
+
+Shapes follow the benchmark configurations; sizes are those the oracle
+finishes in seconds.  Tolerance: |gpu - cpu| <= 2e-5 + 1e-4*|cpu| per element.
+Integer/byte work (the KV append) must be bit-exact.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from util import inv_freq, rmsnorm_heads_np, rope_np, within_tol
+from wick_amd import DeviceKvCache, _native
+
+pytestmark = pytest.mark.gpu
+
+
+def make_inputs(seed, t, start, heads, kv_heads, d, theta=None, qk_norm=False):
+    rng = np.random.default_rng(seed)
+    L = start + t
+    q = rng.standard_normal((t, heads * d), dtype=np.float32)
+    k = rng.standard_normal((L, kv_heads * d), dtype=np.float32)
+    v = rng.standard_normal((L, kv_heads * d), dtype=np.float32)
+    if qk_norm:
+        q = rmsnorm_heads_np(q, heads, d, 1e-6)
+        k = rmsnorm_heads_np(k, kv_heads, d, 1e-6)
+    if theta is not None:
+        inv = inv_freq(theta, d)
+        q = rope_np(q, heads, d, np.arange(start, L), inv)
+        k = rope_np(k, kv_heads, d, np.arange(L), inv)
+    return q, k, v
+
+
+def run_gpu(q, k, v, t, start, heads, kv_heads, d, capacity=None, options=()):
+    L = start + t
+    with DeviceKvCache(1, capacity or L, kv_heads, d) as kv:
+        for opt, val in options:
+            kv.set_option(opt, val)
+        kv.append(0, 0, k[:L], v[:L])
+        return kv.attention(0, heads, q, start)
+
+
+def check(q, k, v, t, start, heads, kv_heads, d, **kw):
+    got = run_gpu(q, k, v, t, start, heads, kv_heads, d, **kw)
+    want = ol.attention(q, k, v, t, start, heads, kv_heads, d)
+    ok, mabs, mrel = within_tol(got, want)
+    print(f"t={t} start={start} Hq={heads} Hkv={kv_heads} d={d}: max abs {mabs:.2e} max rel {mrel:.2e}")
+    assert ok, f"max abs {mabs:.3e}, max rel {mrel:.3e}"
+    return got
+
+
+# ---- decode (t = 1): config 2 (Qwen2.5 shape), config 5 (Llama-3-8B shape), config 1 (SmolLM2 shape)
+
+@pytest.mark.parametrize("L", [512, 4096, 32768])
+def test_decode_qwen25_shape(L):
+    q, k, v = make_inputs(2, 1, L - 1, 14, 2, 64, theta=1e6)
+    check(q, k, v, 1, L - 1, 14, 2, 64)
+
+
+def test_decode_llama3_8b_shape_65536():
+    q, k, v = make_inputs(5, 1, 65535, 32, 8, 128, theta=500000.0)
+    check(q, k, v, 1, 65535, 32, 8, 128)
+
+
+@pytest.mark.parametrize("L", [1, 2, 15, 16, 17, 63, 64, 65, 129, 1000, 4097])
+@pytest.mark.parametrize("d", [16, 32, 64, 128])
+def test_decode_lengths_and_head_dims(L, d):
+    q, k, v = make_inputs(L * 7 + d, 1, L - 1, 9, 3, d)
+    check(q, k, v, 1, L - 1, 9, 3, d)
+
+
+@pytest.mark.parametrize("chunk", [64, 128, 192, 256, 1024, 4096])
+def test_decode_chunk_sizes(chunk):
+    # chunk counts from 1 (single workgroup) through one and two merge levels
+    L = 8191
+    q, k, v = make_inputs(11, 1, L - 1, 14, 2, 64)
+    check(q, k, v, 1, L - 1, 14, 2, 64, options=[(_native.OPT_DECODE_CHUNK, chunk)])
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(40, 2), (16, 1), (8, 8), (7, 7), (33, 1)])
+def test_decode_group_sizes(heads, kv_heads):
+    # group > 16 needs several 16-head slices per kv head
+    L = 3000
+    q, k, v = make_inputs(heads, 1, L - 1, heads, kv_heads, 64)
+    check(q, k, v, 1, L - 1, heads, kv_heads, 64)
+
+
+def test_decode_len1_is_v0_exactly():
+    q, k, v = make_inputs(1, 1, 0, 14, 2, 64)
+    got = run_gpu(q, k, v, 1, 0, 14, 2, 64).reshape(14, 64)
+    for h in range(14):
+        assert np.array_equal(got[h], v[0].reshape(2, 64)[h // 7])
+
+
+def test_decode_bit_stable_and_capacity_larger_than_len():
+    L = 20000
+    q, k, v = make_inputs(4, 1, L - 1, 14, 2, 64)
+    a = run_gpu(q, k, v, 1, L - 1, 14, 2, 64, capacity=L + 333)
+    with DeviceKvCache(1, L + 333, 2, 64) as kv:
+        kv.append(0, 0, k, v)
+        outs = [kv.attention(0, 14, q, L - 1) for _ in range(3)]
+    for o in outs:
+        assert np.array_equal(o, a)
+    want = ol.attention(q, k, v, 1, L - 1, 14, 2, 64)
+    assert within_tol(a, want)[0]
+
+
+# ---- prefill: config 3 (Qwen3 shape with QK-norm), config 4 (TinyLlama chunked), config 1 (SmolLM2)
+
+@pytest.mark.parametrize("T", [512, 2048])
+def test_prefill_qwen3_shape(T):
+    q, k, v = make_inputs(3, T, 0, 16, 8, 128, theta=1e6, qk_norm=True)
+    check(q, k, v, T, 0, 16, 8, 128)
+
+
+def test_chunked_prefill_tinyllama_shape():
+    """1536 cached positions, 512 appended: appended cache bit-exact, output within tolerance."""
+    heads, kvh, d, S, t = 32, 4, 64, 1536, 512
+    q, k, v = make_inputs(4, t, S, heads, kvh, d, theta=10000.0)
+    with DeviceKvCache(2, S + t, kvh, d) as kv:
+        kv.append(1, 0, k[:S], v[:S])
+        kv.append(1, S, k[S:], v[S:])
+        kr, vr = kv.read(1, 0, S + t)
+        assert np.array_equal(kr, k) and np.array_equal(vr, v)
+        got = kv.attention(1, heads, q, S)
+    want = ol.attention(q, k, v, t, S, heads, kvh, d)
+    ok, mabs, mrel = within_tol(got, want)
+    assert ok, (mabs, mrel)
+
+
+def test_prefill_smollm2_shape():
+    q, k, v = make_inputs(1, 128, 0, 9, 3, 64, theta=10000.0)
+    check(q, k, v, 128, 0, 9, 3, 64)
+
+
+@pytest.mark.parametrize("t,start", [(2, 0), (3, 5), (5, 1), (7, 3), (13, 15), (15, 33), (17, 0), (33, 100), (100, 7)])
+@pytest.mark.parametrize("d", [16, 32, 64, 128])
+def test_prefill_ragged(t, start, d):
+    q, k, v = make_inputs(t * 31 + start + d, t, start, 4, 2, d)
+    check(q, k, v, t, start, 4, 2, d)
+
+
+@pytest.mark.parametrize("pairing", [0, 1])
+@pytest.mark.parametrize("heads,kv_heads", [(9, 3), (14, 2), (32, 4), (6, 6)])
+def test_prefill_pairing_and_groups(pairing, heads, kv_heads):
+    t, start = 300, 20
+    q, k, v = make_inputs(heads + pairing, t, start, heads, kv_heads, 64)
+    check(q, k, v, t, start, heads, kv_heads, 64, options=[(_native.OPT_PREFILL_PAIRING, pairing)])
+
+
+def test_prefill_bit_stable():
+    q, k, v = make_inputs(8, 700, 0, 16, 8, 128)
+    a = run_gpu(q, k, v, 700, 0, 16, 8, 128)
+    b = run_gpu(q, k, v, 700, 0, 16, 8, 128)
+    assert np.array_equal(a, b)
+
+
+def test_incremental_chunks_match_one_batch():
+    """The tests/tiny_models.rs:73-95 property on the device cache: chunks vs one batch."""
+    heads, kvh, d = 4, 2, 32
+    sizes = [1, 5, 2, 7, 1, 1, 13, 3, 15]
+    T = sum(sizes)
+    q, k, v = make_inputs(12, T, 0, heads, kvh, d, theta=1e6)
+    batch = run_gpu(q, k, v, T, 0, heads, kvh, d)
+    with DeviceKvCache(1, 256, kvh, d) as kv:
+        pos = 0
+        for s in sizes:
+            kv.append(0, pos, k[pos:pos + s], v[pos:pos + s])
+            rows = kv.attention(0, heads, q[pos:pos + s], pos)
+            assert np.abs(rows - batch[pos:pos + s]).max() < 1e-5
+            pos += s
+
+
+# ---- errors: checked on the host, nothing launched
+
+def test_errors_are_reported():
+    with DeviceKvCache(2, 64, 2, 64) as kv:
+        with pytest.raises(_native.WickHipError) as e:
+            kv.attention(0, 5, np.zeros((1, 5 * 64), np.float32), 0)
+        assert e.value.code == _native.EINVAL and "multiple" in str(e.value)
+        with pytest.raises(_native.WickHipError):
+            kv.attention(0, 4, np.zeros((4, 4 * 64), np.float32), 61)
+        with pytest.raises(_native.WickHipError):
+            kv.attention(2, 4, np.zeros((1, 4 * 64), np.float32), 0)
+        with pytest.raises(_native.WickHipError):
+            kv.append(0, 60, np.zeros((5, 128), np.float32), np.zeros((5, 128), np.float32))
+        with pytest.raises(_native.WickHipError):
+            kv.set_option(_native.OPT_DECODE_CHUNK, 100)

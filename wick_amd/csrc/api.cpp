@@ -1,0 +1,347 @@
+// api.cpp -- the C ABI of include/wick_hip.h over the HIP kernels.
+//
+// Every entry point validates its arguments on the host before anything is
+// launched (a kernel never sees a shape it was not written for), turns HIP
+// failures into status codes, and records a message for wick_hip_last_error().
+#include "wick_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "attn_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(e == hipErrorOutOfMemory ? WICK_HIP_ENOMEM : WICK_HIP_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr)                                   \
+    do {                                                \
+        hipError_t e_ = (expr);                         \
+        if (e_ != hipSuccess) return hip_fail(e_, #expr); \
+    } while (0)
+
+bool supported_head_dim(int d) { return d == 16 || d == 32 || d == 64 || d == 128; }
+
+}  // namespace
+
+struct wick_hip_kv {
+    int layers = 0, capacity = 0, kv_heads = 0, head_dim = 0;
+    int device = 0, num_cus = 256;
+    float *k = nullptr, *v = nullptr;  // [layers][kv_heads][capacity][head_dim]
+    hipStream_t own_stream = nullptr, stream = nullptr;
+    // staging for the host-pointer entry points
+    float *q_dev = nullptr, *att_dev = nullptr, *kst_dev = nullptr, *vst_dev = nullptr;
+    size_t q_cap = 0, att_cap = 0, kst_cap = 0;
+    // decode split-K workspace
+    float *part = nullptr;
+    int *counters = nullptr;
+    int ws_units = 0;
+    // options
+    int decode_chunk = 0, pairing = -1, last_grid = 0;
+
+    size_t layer_floats() const { return (size_t)kv_heads * capacity * head_dim; }
+    float *k_layer(int l) const { return k + (size_t)l * layer_floats(); }
+    float *v_layer(int l) const { return v + (size_t)l * layer_floats(); }
+};
+
+namespace {
+
+int grow(float **buf, size_t *cap, size_t need, const char *what) {
+    if (need <= *cap) return WICK_HIP_OK;
+    if (*buf) (void)hipFree(*buf);
+    *buf = nullptr;
+    *cap = 0;
+    hipError_t e = hipMalloc(buf, need * sizeof(float));
+    if (e != hipSuccess) return hip_fail(e, what);
+    *cap = need;
+    return WICK_HIP_OK;
+}
+
+// Decode workspace for `units` (kv head, 16-head slice) pairs; counters start
+// at zero and every launch leaves them at zero.
+int ensure_workspace(wick_hip_kv *kv, int units) {
+    if (units <= kv->ws_units) return WICK_HIP_OK;
+    if (kv->part) (void)hipFree(kv->part);
+    if (kv->counters) (void)hipFree(kv->counters);
+    kv->part = nullptr;
+    kv->counters = nullptr;
+    kv->ws_units = 0;
+    HIP_TRY(hipMalloc(&kv->part, wick::decode_workspace_floats(units, kv->head_dim) * sizeof(float)));
+    const size_t ncnt = (size_t)units * (wick::kDecodeFan + 1);
+    HIP_TRY(hipMalloc(&kv->counters, ncnt * sizeof(int)));
+    HIP_TRY(hipMemsetAsync(kv->counters, 0, ncnt * sizeof(int), kv->stream));
+    kv->ws_units = units;
+    return WICK_HIP_OK;
+}
+
+int check_kv(const wick_hip_kv *kv, int layer) {
+    if (!kv) return fail(WICK_HIP_EINVAL, "null cache handle");
+    if (layer < 0 || layer >= kv->layers) return fail(WICK_HIP_EINVAL, "layer %d out of range [0, %d)", layer, kv->layers);
+    return WICK_HIP_OK;
+}
+
+int check_span(const wick_hip_kv *kv, int start, int t) {
+    if (t < 1) return fail(WICK_HIP_EINVAL, "t must be >= 1 (got %d)", t);
+    if (start < 0 || (long long)start + t > kv->capacity)
+        return fail(WICK_HIP_EINVAL, "positions %d..%lld exceed the cache capacity %d", start, (long long)start + t,
+                    kv->capacity);
+    return WICK_HIP_OK;
+}
+
+int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int t, int start, float *att_dev) {
+    const int D = kv->head_dim;
+    if (heads < 1 || heads % kv->kv_heads != 0)
+        return fail(WICK_HIP_EINVAL, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv->kv_heads);
+    const int group = heads / kv->kv_heads;
+    const float scale = 1.0f / sqrtf((float)D);  // src/model.rs:527
+
+    if (t == 1) {
+        const int len = start + 1;
+        const int hslices = (group + wick::kTileRows - 1) / wick::kTileRows;
+        const int units = kv->kv_heads * hslices;
+        int rc = ensure_workspace(kv, units);
+        if (rc) return rc;
+        int chunk = kv->decode_chunk;
+        if (chunk <= 0) {
+            // Aim at two workgroups per CU, in whole 64-key steps.
+            const int target = std::max(1, (2 * kv->num_cus + units - 1) / units);
+            chunk = (len + target - 1) / target;
+        }
+        chunk = std::max(64, (chunk + 63) / 64 * 64);
+        const int min_chunk = (len + wick::kDecodeMaxChunks - 1) / wick::kDecodeMaxChunks;
+        if (chunk < min_chunk) chunk = (min_chunk + 63) / 64 * 64;
+        const int nchunks = (len + chunk - 1) / chunk;
+        wick::DecodeArgs a{};
+        a.q = q_dev;
+        a.k = kv->k_layer(layer);
+        a.v = kv->v_layer(layer);
+        a.att = att_dev;
+        a.part = kv->part;
+        a.counters = kv->counters;
+        a.capacity = kv->capacity;
+        a.len = len;
+        a.kv_heads = kv->kv_heads;
+        a.group = group;
+        a.hslices = hslices;
+        a.chunk = chunk;
+        a.nchunks = nchunks;
+        a.ngroups = (nchunks + wick::kDecodeFan - 1) / wick::kDecodeFan;
+        a.scale = scale;
+        const int grid = units * nchunks;
+        kv->last_grid = grid;
+        hipError_t e = wick::launch_decode(D, a, grid, kv->stream);
+        if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
+        return WICK_HIP_OK;
+    }
+
+    wick::PrefillArgs a{};
+    a.q = q_dev;
+    a.k = kv->k_layer(layer);
+    a.v = kv->v_layer(layer);
+    a.att = att_dev;
+    a.capacity = kv->capacity;
+    a.t = t;
+    a.start = start;
+    a.kv_heads = kv->kv_heads;
+    a.group = group;
+    a.nblocks = (t * group + wick::kTileRows - 1) / wick::kTileRows;
+    int paired = kv->pairing;
+    if (paired < 0) {
+        // Pair causal row blocks when the triangle dominates (short prefix) and
+        // there are enough blocks to keep every SIMD busy after halving.
+        const long long waves_unpaired = (long long)a.nblocks * kv->kv_heads;
+        paired = (start < t && waves_unpaired >= 2LL * 4 * kv->num_cus) ? 1 : 0;
+    }
+    a.paired = paired;
+    a.items = paired ? (a.nblocks + 1) / 2 : a.nblocks;
+    a.scale = scale;
+    const int grid = kv->kv_heads * ((a.items + 3) / 4);
+    kv->last_grid = grid;
+    hipError_t e = wick::launch_prefill(D, a, grid, kv->stream);
+    if (e != hipSuccess) return hip_fail(e, "prefill kernel launch");
+    return WICK_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *wick_hip_last_error(void) { return g_last_error.c_str(); }
+
+int wick_hip_kv_create(int layers, int capacity, int kv_heads, int head_dim, wick_hip_kv **out) {
+    if (!out) return fail(WICK_HIP_EINVAL, "null output pointer");
+    *out = nullptr;
+    if (layers < 1 || capacity < 1 || kv_heads < 1)
+        return fail(WICK_HIP_EINVAL, "layers, capacity and kv_heads must be >= 1");
+    if (!supported_head_dim(head_dim)) return fail(WICK_HIP_EINVAL, "head_dim %d not supported (16, 32, 64, 128)", head_dim);
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) return fail(WICK_HIP_EDEVICE, "no HIP device");
+    wick_hip_kv *kv = new wick_hip_kv();
+    kv->layers = layers;
+    kv->capacity = capacity;
+    kv->kv_heads = kv_heads;
+    kv->head_dim = head_dim;
+    int rc = WICK_HIP_OK;
+    hipError_t e;
+    do {
+        if ((e = hipGetDevice(&kv->device)) != hipSuccess) { rc = hip_fail(e, "hipGetDevice"); break; }
+        hipDeviceProp_t prop;
+        if ((e = hipGetDeviceProperties(&prop, kv->device)) != hipSuccess) { rc = hip_fail(e, "hipGetDeviceProperties"); break; }
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+            rc = fail(WICK_HIP_EDEVICE, "device %d is %s; this library is built for gfx950", kv->device, prop.gcnArchName);
+            break;
+        }
+        kv->num_cus = prop.multiProcessorCount;
+        if ((e = hipStreamCreateWithFlags(&kv->own_stream, hipStreamNonBlocking)) != hipSuccess) { rc = hip_fail(e, "hipStreamCreate"); break; }
+        kv->stream = kv->own_stream;
+        const size_t bytes = (size_t)layers * kv->layer_floats() * sizeof(float);
+        if ((e = hipMalloc(&kv->k, bytes)) != hipSuccess) { rc = hip_fail(e, "hipMalloc(K cache)"); break; }
+        if ((e = hipMalloc(&kv->v, bytes)) != hipSuccess) { rc = hip_fail(e, "hipMalloc(V cache)"); break; }
+        // KvCache::new zero-fills (src/model.rs:265-266)
+        if ((e = hipMemsetAsync(kv->k, 0, bytes, kv->stream)) != hipSuccess) { rc = hip_fail(e, "hipMemset(K)"); break; }
+        if ((e = hipMemsetAsync(kv->v, 0, bytes, kv->stream)) != hipSuccess) { rc = hip_fail(e, "hipMemset(V)"); break; }
+        if ((e = hipStreamSynchronize(kv->stream)) != hipSuccess) { rc = hip_fail(e, "hipStreamSynchronize"); break; }
+    } while (0);
+    if (rc != WICK_HIP_OK) {
+        wick_hip_kv_destroy(kv);
+        return rc;
+    }
+    *out = kv;
+    return WICK_HIP_OK;
+}
+
+void wick_hip_kv_destroy(wick_hip_kv *kv) {
+    if (!kv) return;
+    if (kv->stream) (void)hipStreamSynchronize(kv->stream);
+    float *bufs[] = {kv->k, kv->v, kv->q_dev, kv->att_dev, kv->kst_dev, kv->vst_dev, kv->part};
+    for (float *b : bufs)
+        if (b) (void)hipFree(b);
+    if (kv->counters) (void)hipFree(kv->counters);
+    if (kv->own_stream) (void)hipStreamDestroy(kv->own_stream);
+    delete kv;
+}
+
+int wick_hip_kv_set_stream(wick_hip_kv *kv, void *stream) {
+    if (!kv) return fail(WICK_HIP_EINVAL, "null cache handle");
+    kv->stream = stream ? (hipStream_t)stream : kv->own_stream;
+    return WICK_HIP_OK;
+}
+
+int wick_hip_kv_synchronize(wick_hip_kv *kv) {
+    if (!kv) return fail(WICK_HIP_EINVAL, "null cache handle");
+    HIP_TRY(hipStreamSynchronize(kv->stream));
+    return WICK_HIP_OK;
+}
+
+int wick_hip_kv_set_option(wick_hip_kv *kv, int option, int value) {
+    if (!kv) return fail(WICK_HIP_EINVAL, "null cache handle");
+    switch (option) {
+    case WICK_HIP_OPT_DECODE_CHUNK:
+        if (value < 0 || value % 64 != 0) return fail(WICK_HIP_EINVAL, "decode chunk must be 0 or a multiple of 64");
+        kv->decode_chunk = value;
+        return WICK_HIP_OK;
+    case WICK_HIP_OPT_PREFILL_PAIRING:
+        if (value < -1 || value > 1) return fail(WICK_HIP_EINVAL, "pairing must be -1, 0 or 1");
+        kv->pairing = value;
+        return WICK_HIP_OK;
+    default:
+        return fail(WICK_HIP_EINVAL, "unknown option %d", option);
+    }
+}
+
+int wick_hip_kv_last_grid(const wick_hip_kv *kv) { return kv ? kv->last_grid : 0; }
+
+int wick_hip_kv_append_device(wick_hip_kv *kv, int layer, int start, int t, const float *k_dev, const float *v_dev) {
+    int rc = check_kv(kv, layer);
+    if (rc) return rc;
+    if ((rc = check_span(kv, start, t))) return rc;
+    if (!k_dev || !v_dev) return fail(WICK_HIP_EINVAL, "null k or v");
+    wick::AppendArgs a{k_dev, v_dev, kv->k_layer(layer), kv->v_layer(layer), kv->capacity, start, t, kv->kv_heads};
+    hipError_t e = wick::launch_append(kv->head_dim, a, kv->stream);
+    if (e != hipSuccess) return hip_fail(e, "append kernel launch");
+    return WICK_HIP_OK;
+}
+
+int wick_hip_kv_append(wick_hip_kv *kv, int layer, int start, int t, const float *k, const float *v) {
+    int rc = check_kv(kv, layer);
+    if (rc) return rc;
+    if ((rc = check_span(kv, start, t))) return rc;
+    if (!k || !v) return fail(WICK_HIP_EINVAL, "null k or v");
+    const size_t n = (size_t)t * kv->kv_heads * kv->head_dim;
+    if (n > kv->kst_cap) {
+        size_t ck = kv->kst_cap, cv = kv->kst_cap;
+        kv->kst_cap = 0;
+        if ((rc = grow(&kv->kst_dev, &ck, n, "hipMalloc(k staging)"))) return rc;
+        if ((rc = grow(&kv->vst_dev, &cv, n, "hipMalloc(v staging)"))) return rc;
+        kv->kst_cap = n;
+    }
+    HIP_TRY(hipMemcpyAsync(kv->kst_dev, k, n * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+    HIP_TRY(hipMemcpyAsync(kv->vst_dev, v, n * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+    if ((rc = wick_hip_kv_append_device(kv, layer, start, t, kv->kst_dev, kv->vst_dev))) return rc;
+    HIP_TRY(hipStreamSynchronize(kv->stream));
+    return WICK_HIP_OK;
+}
+
+int wick_hip_kv_read(const wick_hip_kv *kv, int layer, int pos0, int n, float *k, float *v) {
+    int rc = check_kv(kv, layer);
+    if (rc) return rc;
+    if ((rc = check_span(kv, pos0, n))) return rc;
+    const int D = kv->head_dim, kvd = kv->kv_heads * D;
+    for (int h = 0; h < kv->kv_heads; h++) {
+        const size_t off = ((size_t)h * kv->capacity + pos0) * D;
+        if (k)
+            HIP_TRY(hipMemcpy2DAsync(k + (size_t)h * D, kvd * sizeof(float), kv->k_layer(layer) + off, D * sizeof(float),
+                                     D * sizeof(float), n, hipMemcpyDeviceToHost, kv->stream));
+        if (v)
+            HIP_TRY(hipMemcpy2DAsync(v + (size_t)h * D, kvd * sizeof(float), kv->v_layer(layer) + off, D * sizeof(float),
+                                     D * sizeof(float), n, hipMemcpyDeviceToHost, kv->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(kv->stream));
+    return WICK_HIP_OK;
+}
+
+int wick_hip_attention_device(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int t, int start,
+                              float *att_dev) {
+    int rc = check_kv(kv, layer);
+    if (rc) return rc;
+    if ((rc = check_span(kv, start, t))) return rc;
+    if (!q_dev || !att_dev) return fail(WICK_HIP_EINVAL, "null q or att");
+    return run_attention(kv, layer, heads, q_dev, t, start, att_dev);
+}
+
+int wick_hip_attention(wick_hip_kv *kv, int layer, int heads, const float *q, int t, int start, float *att) {
+    int rc = check_kv(kv, layer);
+    if (rc) return rc;
+    if ((rc = check_span(kv, start, t))) return rc;
+    if (!q || !att) return fail(WICK_HIP_EINVAL, "null q or att");
+    if (heads < 1) return fail(WICK_HIP_EINVAL, "heads must be >= 1");
+    const size_t n = (size_t)t * heads * kv->head_dim;
+    if ((rc = grow(&kv->q_dev, &kv->q_cap, n, "hipMalloc(q staging)"))) return rc;
+    if ((rc = grow(&kv->att_dev, &kv->att_cap, n, "hipMalloc(att staging)"))) return rc;
+    HIP_TRY(hipMemcpyAsync(kv->q_dev, q, n * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+    if ((rc = run_attention(kv, layer, heads, kv->q_dev, t, start, kv->att_dev))) return rc;
+    HIP_TRY(hipMemcpyAsync(att, kv->att_dev, n * sizeof(float), hipMemcpyDeviceToHost, kv->stream));
+    HIP_TRY(hipStreamSynchronize(kv->stream));
+    return WICK_HIP_OK;
+}
+
+}  // extern "C"

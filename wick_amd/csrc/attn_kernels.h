@@ -1,0 +1,50 @@
+// Internal interface between the C ABI (api.cpp) and the HIP kernels
+// (attention.hip).  Not installed; the public boundary is include/wick_hip.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+namespace wick {
+
+// Decode workgroups merge their partial softmax states in a tree of fan-in
+// kDecodeFan (two levels at most), so one call handles at most
+// kDecodeFan * kDecodeFan chunks per (kv head, head slice).
+constexpr int kDecodeFan = 16;
+constexpr int kDecodeMaxChunks = kDecodeFan * kDecodeFan;
+constexpr int kTileRows = 16;  // query rows (or heads) per MFMA column block
+
+struct DecodeArgs {
+    const float *q;   // [heads*D] (one token)
+    const float *k;   // layer base, [kv_heads][capacity][D]
+    const float *v;
+    float *att;       // [heads*D]
+    float *part;      // partial states, see decode_workspace_floats
+    int *counters;    // [units][kDecodeFan + 1], zero between launches
+    int capacity, len, kv_heads, group, hslices, chunk, nchunks, ngroups;
+    float scale;
+};
+
+struct PrefillArgs {
+    const float *q;   // [t][heads*D]
+    const float *k;   // layer base, [kv_heads][capacity][D]
+    const float *v;
+    float *att;       // [t][heads*D]
+    int capacity, t, start, kv_heads, group, nblocks, items, paired;
+    float scale;
+};
+
+struct AppendArgs {
+    const float *ksrc, *vsrc;  // [t][kv_heads*D]
+    float *k, *v;              // layer base, [kv_heads][capacity][D]
+    int capacity, start, t, kv_heads;
+};
+
+// Floats of decode workspace needed for `units` (kv head, head slice) pairs.
+size_t decode_workspace_floats(int units, int head_dim);
+
+hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_t s);
+hipError_t launch_prefill(int head_dim, const PrefillArgs &a, int grid, hipStream_t s);
+hipError_t launch_append(int head_dim, const AppendArgs &a, hipStream_t s);
+
+}  // namespace wick
