@@ -1,0 +1,252 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention path (one JSON line on stdout).
+
+Workload: decode attention, Qwen2.5-0.5B shape --
+14 query heads / 2 KV heads, head_dim 64, f32, 24 layers, one new query token
+per layer over a KV cache of 32768 positions per layer.  One step = the decode
+attention of all 24 layers (24 launches, one per layer, each over its own
+33.5 MB of K+V, so the 805 MB working set streams from HBM rather than from
+the 256 MB Infinity Cache).  Inputs are resident in HBM before timing starts.
+
+value  = algorithmic bytes per step / step time, in GB/s, where one layer
+         reads 4*(2*L*Hkv*d + 2*Hq*d) bytes (K, V, q, and writes att).
+Also reported: causal prefill TFLOP/s (configs[2], Qwen3 shape, T = 2048) and
+the CPU oracle timed on the host cores on a bounded sample (cpu_baseline).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+F32_MFMA_PEAK_TFLOPS = 157.3
+
+DEC = dict(heads=14, kv_heads=2, d=64, layers=24, L=32768, theta=1e6, seed=2)
+PRE = dict(heads=16, kv_heads=8, d=128, T=2048, theta=1e6, seed=3, eps=1e-6)
+
+
+def decode_bytes(L, heads, kv_heads, d):
+    return 4 * (2 * L * kv_heads * d + 2 * heads * d)
+
+
+def prefill_flops(T, heads, d, start=0):
+    # 2 matmuls x 2 flops per MAC over the causal (i, p <= start+i) pairs
+    return 4 * d * heads * sum(start + i + 1 for i in range(T))
+
+
+def rope_torch(x, heads, d, positions, inv_freq):
+    import torch
+    n = x.shape[0]
+    x = x.view(n, heads, d)
+    half = d // 2
+    ang = positions.to(torch.float32)[:, None] * inv_freq[None, :]
+    s, c = torch.sin(ang)[:, None, :], torch.cos(ang)[:, None, :]
+    a, b = x[..., :half].clone(), x[..., half:].clone()
+    x[..., :half] = a * c - b * s
+    x[..., half:] = b * c + a * s
+    return x.view(n, heads * d)
+
+
+def inv_freq_torch(theta, d, dev):
+    import torch
+    return torch.tensor([1.0 / theta ** (2.0 * i / d) for i in range(d // 2)], dtype=torch.float32, device=dev)
+
+
+def setup_decode(torch, kv_cls, dev):
+    c = DEC
+    g = torch.Generator(device=dev)
+    g.manual_seed(c["seed"])
+    inv = inv_freq_torch(c["theta"], c["d"], dev)
+    kv = kv_cls(c["layers"], c["L"], c["kv_heads"], c["d"])
+    kv.set_stream(torch.cuda.current_stream().cuda_stream)
+    pos = torch.arange(c["L"], device=dev)
+    for layer in range(c["layers"]):
+        k = torch.randn(c["L"], c["kv_heads"] * c["d"], generator=g, device=dev)
+        v = torch.randn(c["L"], c["kv_heads"] * c["d"], generator=g, device=dev)
+        k = rope_torch(k, c["kv_heads"], c["d"], pos, inv).contiguous()
+        kv.append_device(layer, 0, c["L"], k.data_ptr(), v.data_ptr())
+        torch.cuda.synchronize()
+        del k, v
+    q = torch.randn(c["layers"], c["heads"] * c["d"], generator=g, device=dev)
+    q = rope_torch(q, c["heads"], c["d"], torch.full((c["layers"],), c["L"] - 1, device=dev), inv).contiguous()
+    att = torch.empty_like(q)
+    return kv, q, att
+
+
+def time_launches(torch, fn, launches_per_step, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    e1.synchronize()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    return ms / steps, ms / (steps * launches_per_step)
+
+
+def cpu_baseline_decode(kv, q_host, threads, budget_s=12.0, max_reps=7):
+    """wick's CPU attention (the oracle) on the host: decode over all 24 layers, median of reps."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import numpy as np
+    import oracle_lib as ol
+    c = DEC
+    layers = []
+    for layer in range(c["layers"]):
+        k, v = kv.read(layer, 0, c["L"])
+        layers.append((k, v))
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < max_reps and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        for layer in range(c["layers"]):
+            k, v = layers[layer]
+            ol.attention(q_host[layer:layer + 1], k, v, 1, c["L"] - 1, c["heads"], c["kv_heads"], c["d"],
+                         threads=threads)
+        times.append(time.perf_counter() - t0)
+    step_s = float(np.median(times))
+    return step_s, len(times)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--decode-chunk", type=int, default=0)
+    ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(sharding is described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from wick_amd import DeviceKvCache, _native
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    # One explicit stream for everything: the library launches on it and the
+    # HIP events that time the kernels are recorded on it.
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    c = DEC
+
+    # ---------------- decode (the headline)
+    kv, q, att = setup_decode(torch, DeviceKvCache, dev)
+    if args.decode_chunk:
+        kv.set_option(_native.OPT_DECODE_CHUNK, args.decode_chunk)
+    hd, qd = c["heads"] * c["d"], c["heads"] * c["d"]
+    qp, ap_ = q.data_ptr(), att.data_ptr()
+
+    def step():
+        for layer in range(c["layers"]):
+            kv.attention_device(layer, c["heads"], qp + 4 * qd * layer, 1, c["L"] - 1, ap_ + 4 * hd * layer)
+
+    ms_step_eager, ms_launch_eager = time_launches(torch, step, c["layers"], args.steps, args.warmup)
+    mode = "eager"
+    ms_step, ms_launch = ms_step_eager, ms_launch_eager
+    if not args.eager:
+        # One step (24 launches) captured as a HIP graph and replayed: the way a
+        # GPU-resident decode loop issues its per-token work.  The decode kernel
+        # resets its own merge counters, so replays need no memset nodes.
+        graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+        torch.cuda.synchronize()
+        ms_step, ms_launch = time_launches(torch, graph.replay, c["layers"], args.steps, args.warmup)
+        mode = "hip-graph"
+    grid = kv.last_grid()
+    bytes_layer = decode_bytes(c["L"], c["heads"], c["kv_heads"], c["d"])
+    bytes_step = bytes_layer * c["layers"]
+    value = bytes_step / (ms_step * 1e-3) / 1e9
+    achieved = bytes_layer / (ms_launch * 1e-3) / 1e9
+
+    out = {
+        "metric": "decode-attn HBM GB/s (% peak) @32K ctx; prefill-attn TFLOP/s; e2e decode tok/s",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "decode attention, Qwen2.5-0.5B shape (Hq 14 / Hkv 2, head_dim 64), 24 layers, "
+                               "KV cache 32768 positions per layer, f32, one query token per layer",
+                   "layers_per_step": c["layers"], "context": c["L"], "decode_workgroups": grid,
+                   "launch": mode, "eager_ms_per_step": round(ms_step_eager, 4)},
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "kernel": "wick::decode_kernel<64>", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": bytes_layer, "us_per_launch": round(ms_launch * 1e3, 3)},
+    }
+
+    # ---------------- prefill (configs[2], T = 2048)
+    if not args.no_prefill:
+        p = PRE
+        g = torch.Generator(device=dev)
+        g.manual_seed(p["seed"])
+        inv = inv_freq_torch(p["theta"], p["d"], dev)
+        T = p["T"]
+
+        def qknorm(x, heads):
+            x = x.view(T, heads, p["d"])
+            return (x * torch.rsqrt((x * x).mean(-1, keepdim=True) + p["eps"])).view(T, heads * p["d"])
+        pos = torch.arange(T, device=dev)
+        pq = rope_torch(qknorm(torch.randn(T, p["heads"] * p["d"], generator=g, device=dev), p["heads"]),
+                        p["heads"], p["d"], pos, inv).contiguous()
+        pk = rope_torch(qknorm(torch.randn(T, p["kv_heads"] * p["d"], generator=g, device=dev), p["kv_heads"]),
+                        p["kv_heads"], p["d"], pos, inv).contiguous()
+        pv = torch.randn(T, p["kv_heads"] * p["d"], generator=g, device=dev)
+        patt = torch.empty_like(pq)
+        pkv = DeviceKvCache(1, T, p["kv_heads"], p["d"])
+        pkv.set_stream(torch.cuda.current_stream().cuda_stream)
+        pkv.append_device(0, 0, T, pk.data_ptr(), pv.data_ptr())
+
+        def pstep():
+            pkv.attention_device(0, p["heads"], pq.data_ptr(), T, 0, patt.data_ptr())
+        psteps = max(5, args.steps // 10)
+        ms_p, _ = time_launches(torch, pstep, 1, psteps, max(2, args.warmup // 5))
+        fl = prefill_flops(T, p["heads"], p["d"])
+        tf = fl / (ms_p * 1e-3) / 1e12
+        out["prefill_tflops"] = round(tf, 2)
+        out["roofline_prefill"] = {"bound": "mfma", "kernel": "wick::prefill_kernel<128>", "achieved": round(tf, 2),
+                                   "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                   "frac": round(tf / F32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                                   "flops_per_launch": fl, "us_per_launch": round(ms_p * 1e3, 2),
+                                   "workload": "causal prefill, Qwen3-0.6B shape (Hq 16 / Hkv 8, d 128), T 2048, "
+                                               "QK-norm + RoPE applied, empty cache"}
+        pkv.close()
+
+    # ---------------- CPU baseline (oracle on the host cores, bounded sample)
+    if not args.no_cpu:
+        threads = os.cpu_count() or 1
+        step_s, reps = cpu_baseline_decode(kv, q.cpu().numpy(), threads)
+        cpu_gbs = bytes_step / step_s / 1e9
+        out["cpu_baseline"] = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+                               "sample": f"wick's CPU attention restated in C (AVX2 order), all 24 decode layers at "
+                                         f"L=32768 on the host, median of {reps} full steps "
+                                         f"({step_s * 1e3:.1f} ms/step; {c['heads']} (token, head) items per layer "
+                                         f"over a {threads}-thread pool)",
+                               "ms_per_step": round(step_s * 1e3, 2)}
+    kv.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -68,12 +68,43 @@ def test_decode_lengths_and_head_dims(L, d):
     check(q, k, v, 1, L - 1, 9, 3, d)
 
 
-@pytest.mark.parametrize("chunk", [64, 128, 192, 256, 1024, 4096])
-def test_decode_chunk_sizes(chunk):
-    # chunk counts from 1 (single workgroup) through one and two merge levels
+@pytest.mark.parametrize("merge", [0, 1])
+@pytest.mark.parametrize("chunk", [64, 128, 192, 256, 1024, 4096, 8192])
+def test_decode_chunk_sizes(chunk, merge):
+    # chunk counts from 1 (single workgroup) through one and two merge levels,
+    # with the in-kernel merge tree and with the separate merge kernel
     L = 8191
     q, k, v = make_inputs(11, 1, L - 1, 14, 2, 64)
-    check(q, k, v, 1, L - 1, 14, 2, 64, options=[(_native.OPT_DECODE_CHUNK, chunk)])
+    check(q, k, v, 1, L - 1, 14, 2, 64,
+          options=[(_native.OPT_DECODE_CHUNK, chunk), (_native.OPT_DECODE_MERGE, merge)])
+
+
+@pytest.mark.parametrize("merge", [0, 1])
+@pytest.mark.parametrize("d", [16, 32, 64, 128])
+def test_decode_merge_modes_agree(merge, d):
+    L = 5000
+    q, k, v = make_inputs(d + 100 * merge, 1, L - 1, 12, 3, d)
+    check(q, k, v, 1, L - 1, 12, 3, d, options=[(_native.OPT_DECODE_CHUNK, 64), (_native.OPT_DECODE_MERGE, merge)])
+
+
+def test_decode_repeated_launches_reuse_counters():
+    # the merge counters are reset by the kernel itself: many launches in a row
+    # on one handle, alternating layers, must all be right
+    L = 6000
+    with DeviceKvCache(2, L, 2, 64) as kv:
+        kv.set_option(_native.OPT_DECODE_CHUNK, 64)
+        data = []
+        for layer in range(2):
+            q, k, v = make_inputs(40 + layer, 1, L - 1, 14, 2, 64)
+            kv.append(layer, 0, k, v)
+            data.append((q, ol.attention(q, k, v, 1, L - 1, 14, 2, 64)))
+        first = [kv.attention(layer, 14, data[layer][0], L - 1) for layer in range(2)]
+        for it in range(20):
+            layer = it % 2
+            got = kv.attention(layer, 14, data[layer][0], L - 1)
+            assert np.array_equal(got, first[layer])
+        for layer in range(2):
+            assert within_tol(first[layer], data[layer][1])[0]
 
 
 @pytest.mark.parametrize("heads,kv_heads", [(40, 2), (16, 1), (8, 8), (7, 7), (33, 1)])

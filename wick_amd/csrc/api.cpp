@@ -56,7 +56,8 @@ struct wick_hip_kv {
     int *counters = nullptr;
     int ws_units = 0;
     // options
-    int decode_chunk = 0, pairing = -1, last_grid = 0;
+    int decode_chunk = 0, pairing = -1, decode_merge = 0, last_grid = 0;
+    int decode_blocks_per_cu = 1;
 
     size_t layer_floats() const { return (size_t)kv_heads * capacity * head_dim; }
     float *k_layer(int l) const { return k + (size_t)l * layer_floats(); }
@@ -122,8 +123,10 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
         if (rc) return rc;
         int chunk = kv->decode_chunk;
         if (chunk <= 0) {
-            // Aim at two workgroups per CU, in whole 64-key steps.
-            const int target = std::max(1, (2 * kv->num_cus + units - 1) / units);
+            // One resident round: as many chunks as the GPU holds decode
+            // workgroups at once, each streaming one long contiguous range.
+            const int resident = kv->num_cus * kv->decode_blocks_per_cu;
+            const int target = std::max(1, resident / units);
             chunk = (len + target - 1) / target;
         }
         chunk = std::max(64, (chunk + 63) / 64 * 64);
@@ -145,6 +148,7 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
         a.chunk = chunk;
         a.nchunks = nchunks;
         a.ngroups = (nchunks + wick::kDecodeFan - 1) / wick::kDecodeFan;
+        a.merge_mode = kv->decode_merge;
         a.scale = scale;
         const int grid = units * nchunks;
         kv->last_grid = grid;
@@ -211,6 +215,7 @@ int wick_hip_kv_create(int layers, int capacity, int kv_heads, int head_dim, wic
             break;
         }
         kv->num_cus = prop.multiProcessorCount;
+        kv->decode_blocks_per_cu = wick::decode_blocks_per_cu(head_dim);
         if ((e = hipStreamCreateWithFlags(&kv->own_stream, hipStreamNonBlocking)) != hipSuccess) { rc = hip_fail(e, "hipStreamCreate"); break; }
         kv->stream = kv->own_stream;
         const size_t bytes = (size_t)layers * kv->layer_floats() * sizeof(float);
@@ -262,6 +267,10 @@ int wick_hip_kv_set_option(wick_hip_kv *kv, int option, int value) {
     case WICK_HIP_OPT_PREFILL_PAIRING:
         if (value < -1 || value > 1) return fail(WICK_HIP_EINVAL, "pairing must be -1, 0 or 1");
         kv->pairing = value;
+        return WICK_HIP_OK;
+    case WICK_HIP_OPT_DECODE_MERGE:
+        if (value < 0 || value > 1) return fail(WICK_HIP_EINVAL, "decode merge must be 0 or 1");
+        kv->decode_merge = value;
         return WICK_HIP_OK;
     default:
         return fail(WICK_HIP_EINVAL, "unknown option %d", option);

@@ -22,6 +22,7 @@ struct DecodeArgs {
     float *part;      // partial states, see decode_workspace_floats
     int *counters;    // [units][kDecodeFan + 1], zero between launches
     int capacity, len, kv_heads, group, hslices, chunk, nchunks, ngroups;
+    int merge_mode;   // 0: in-kernel merge tree, 1: separate merge kernel
     float scale;
 };
 
@@ -42,6 +43,9 @@ struct AppendArgs {
 
 // Floats of decode workspace needed for `units` (kv head, head slice) pairs.
 size_t decode_workspace_floats(int units, int head_dim);
+
+// Decode workgroups one CU holds at once (from the kernel's register and LDS use).
+int decode_blocks_per_cu(int head_dim);
 
 hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_t s);
 hipError_t launch_prefill(int head_dim, const PrefillArgs &a, int grid, hipStream_t s);
