@@ -124,6 +124,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--decode-chunk", type=int, default=0)
     ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph)")
     args = ap.parse_args()
@@ -232,6 +233,34 @@ def main():
                                    "workload": "causal prefill, Qwen3-0.6B shape (Hq 16 / Hkv 8, d 128), T 2048, "
                                                "QK-norm + RoPE applied, empty cache"}
         pkv.close()
+
+    # ---------------- e2e: wick's forward, attention on the GPU
+    if not args.no_e2e:
+        import numpy as np
+        from wick_amd.host import HostModel
+        from wick_amd.synthetic import random_prompt, random_weights, smollm2_135m
+        cfg = smollm2_135m()
+        w = random_weights(cfg, seed=0)
+        prompt = random_prompt(1, 128, cfg.vocab)
+        hm = HostModel(cfg, w)
+        st = hm.new_state(128 + 64 + 8)
+        hm.forward(st, prompt[:8])  # warm the pool and the device path, as cmd_bench does
+        st.len = 0
+        t0 = time.perf_counter()
+        logits = hm.forward(st, prompt)
+        t1 = time.perf_counter()
+        tok = int(np.argmax(logits[0]))
+        for _ in range(64):
+            logits = hm.forward(st, [tok])
+            tok = int(np.argmax(logits[0]))
+        t2 = time.perf_counter()
+        out["e2e_decode_tok_s"] = round(64 / (t2 - t1), 2)
+        out["e2e"] = {"workload": "random-init SmolLM2-135M architecture, f32, 128-token prompt + 64 greedy tokens "
+                                  "(wick's cmd_bench loop); projections on the host CPU, KV cache + attention on the GPU",
+                      "prompt_tok_s": round(128 / (t1 - t0), 1), "decode_tok_s": round(64 / (t2 - t1), 2),
+                      "host_threads": os.cpu_count()}
+        hm.close()
+        del w
 
     # ---------------- CPU baseline (oracle on the host cores, bounded sample)
     if not args.no_cpu:

@@ -1,0 +1,127 @@
+"""End to end: wick's Model::forward (C++ host mirror) with the KV cache and
+attention on the GPU, checked against the all-CPU oracle forward and against
+the reference's transformers-scored tiny fixtures with the reference's own
+thresholds (tests/tiny_models.rs:58-113)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from util import within_tol
+from wick_amd import DeviceKvCache
+from wick_amd.host import HostModel
+from wick_amd.model import Config, load_weights
+from wick_amd.synthetic import random_prompt, random_weights, smollm2_135m
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny")
+MODELS = ["llama3-scaled-f32", "qwen2-bias-bf16", "qwen3-qknorm-f32"]
+
+
+def fixture(name):
+    d = os.path.join(GOLDEN, name)
+    cfg = Config.load(d)
+    with open(os.path.join(d, "expected.json")) as f:
+        exp = json.load(f)
+    return cfg, load_weights(d, cfg), exp
+
+
+@pytest.mark.parametrize("name", MODELS)
+def test_tiny_matches_transformers(name):
+    cfg, w, exp = fixture(name)
+    m = HostModel(cfg, w, threads=4)
+    got = m.forward(m.new_state(256), exp["tokens"], all_logits=True)
+    worst = np.abs(got - np.array(exp["logits"], np.float32)).max()
+    assert worst < 1e-3, f"{name}: logits differ by {worst}"
+
+
+@pytest.mark.parametrize("name", MODELS)
+def test_tiny_incremental_matches_batch(name):
+    cfg, w, exp = fixture(name)
+    m = HostModel(cfg, w, threads=3)
+    batch = m.forward(m.new_state(256), exp["tokens"], all_logits=True)
+    st = m.new_state(256)
+    pos = 0
+    for size in [1, 5, 2, 7, 1, 1, 13, 3, 15]:
+        rows = m.forward(st, exp["tokens"][pos:pos + size], all_logits=True)
+        d = np.abs(rows - batch[pos:pos + size]).max()
+        assert d < 1e-4, f"{name}: position {pos} differs by {d}"
+        pos += size
+
+
+@pytest.mark.parametrize("name", MODELS)
+def test_tiny_greedy_continuation(name):
+    cfg, w, exp = fixture(name)
+    m = HostModel(cfg, w, threads=2)
+    st = m.new_state(256)
+    logits = m.forward(st, exp["greedy_prompt"])
+    out = []
+    for _ in range(len(exp["greedy"])):
+        tok = int(np.argmax(logits[0]))
+        out.append(tok)
+        logits = m.forward(st, [tok])
+    assert out == exp["greedy"]
+
+
+def test_prefix_reuse_truncates_the_device_cache():
+    """Session::prefill keeps a common prefix by truncating cache.len (src/engine.rs:127-132)."""
+    cfg, w, exp = fixture("qwen2-bias-bf16")
+    m = HostModel(cfg, w, threads=2)
+    toks = exp["tokens"]
+    ref = m.forward(m.new_state(256), toks[:30], all_logits=True)
+    st = m.new_state(256)
+    m.forward(st, toks[:20] + [5, 6, 7], all_logits=True)  # diverges after 20
+    st.len = 20
+    rows = m.forward(st, toks[20:30], all_logits=True)
+    assert np.abs(rows - ref[20:30]).max() < 1e-4
+
+
+def greedy(model, state, prompt, n_gen):
+    logits = model.forward(state, prompt)
+    ids, margins = [], []
+    for _ in range(n_gen):
+        row = logits[0]
+        top2 = np.partition(row, -2)[-2:]
+        margins.append(float(top2[1] - top2[0]))
+        tok = int(np.argmax(row))
+        ids.append(tok)
+        logits = model.forward(state, [tok])
+    return ids, margins
+
+
+def test_smollm2_135m_greedy_ids_match_cpu():
+    """random-init SmolLM2-135M architecture, 128-token prompt, 64 greedy tokens."""
+    cfg = smollm2_135m()
+    w = random_weights(cfg, seed=0)
+    prompt = random_prompt(1, 128, cfg.vocab)
+    om = ol.OracleModel(cfg, w)
+    ost = om.new_state(128 + 64 + 8)
+    logits = om.forward(ost, prompt)
+    want = []
+    for _ in range(64):
+        tok = ol.argmax(logits[0])
+        want.append(tok)
+        logits = om.forward(ost, [tok])
+    hm = HostModel(cfg, w)
+    got, margins = greedy(hm, hm.new_state(128 + 64 + 8), prompt, 64)
+    print("min top-2 margin over the 64 steps:", min(margins))
+    assert got == want
+
+
+def test_smollm2_135m_attention_teacher_forced():
+    """Per-layer attention of the 128-token prefill, both sides fed the CPU run's q and K/V."""
+    cfg = smollm2_135m()
+    w = random_weights(cfg, seed=0)
+    prompt = random_prompt(1, 128, cfg.vocab)
+    om = ol.OracleModel(cfg, w)
+    st = om.new_state(256)
+    _, qt, at = om.forward(st, prompt, trace=True)
+    with DeviceKvCache(cfg.layers, 256, cfg.kv_heads, cfg.head_dim) as kv:
+        for layer in range(cfg.layers):
+            kv.append(layer, 0, st["k"][layer, :128], st["v"][layer, :128])
+            got = kv.attention(layer, cfg.heads, qt[layer], 0)
+            ok, mabs, mrel = within_tol(got, at[layer])
+            assert ok, f"layer {layer}: max abs {mabs:.3e} max rel {mrel:.3e}"

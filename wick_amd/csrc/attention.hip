@@ -183,13 +183,23 @@ __device__ __forceinline__ void compute_tiles(const TileBuf<D> &b, int kbeg, int
 // Stream keys [kbeg, kend) of one kv head through the wave, in groups of TG
 // 16-key tiles: group n covers tiles tile0 + n*tstep .. +TG-1.  Keys at or past
 // klimit (this lane's column limit, <= kend for decode) are masked.  Loads of
-// the next group are issued before the current group is computed.
-template <int D>
+// the next group are issued before the current group is computed (PINGPONG),
+// or each group is loaded then computed with half the registers, which buys
+// more resident waves instead (the better trade for head_dim 128 decode).
+template <int D, bool PINGPONG = true>
 __device__ __forceinline__ void attend_range(const float *__restrict__ Kh, const float *__restrict__ Vh, int kbeg,
                                              int kend, int tile0, int tstep, int klimit, float scale,
                                              const f4 (&q)[Shape<D>::KJ], int lane, WaveState<D> &st) {
     const int ntiles = (kend - kbeg + 15) >> 4;
     klimit = min(klimit, kend);
+    if constexpr (!PINGPONG) {
+        TileBuf<D> b;
+        for (int first = tile0; first < ntiles; first += tstep) {
+            load_tiles<D>(Kh, Vh, kbeg, kend, first, lane, b);
+            compute_tiles<D>(b, kbeg, first, klimit, scale, q, lane, st);
+        }
+        return;
+    }
     TileBuf<D> ba, bb;
     int first = tile0;
     if (first >= ntiles) return;
@@ -374,7 +384,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 
     WaveState<D> st;
     init_state<D>(st);
-    attend_range<D>(Kh, Vh, kbeg, kend, w * S::TG, 4 * S::TG, a.len, a.scale, q, lane, st);
+    attend_range<D, (D < 128)>(Kh, Vh, kbeg, kend, w * S::TG, 4 * S::TG, a.len, a.scale, q, lane, st);
     st.l = col_sum(st.l);
 
     if (g == 0) {
