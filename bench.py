@@ -94,6 +94,24 @@ def time_launches(torch, fn, launches_per_step, steps, warmup):
     return ms / steps, ms / (steps * launches_per_step)
 
 
+COPY_MIB = 256
+
+
+def pmc_case(torch, kv, q, att, dev):
+    """The workload the committed rocprofv3 --pmc summaries are taken on."""
+    c = DEC
+    hd = c["heads"] * c["d"]
+    for layer in range(c["layers"]):
+        kv.attention_device(layer, c["heads"], q.data_ptr() + 4 * hd * layer, 1, c["L"] - 1,
+                            att.data_ptr() + 4 * hd * layer)
+    torch.cuda.synchronize()
+    src = torch.ones(COPY_MIB << 18, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)  # a plain copy of known size: COPY_MIB MiB read + COPY_MIB MiB written
+    torch.cuda.synchronize()
+    print(f"pmc case done: 24 decode launches, copy of {COPY_MIB} MiB", flush=True)
+
+
 def cpu_baseline_decode(kv, q_host, threads, budget_s=12.0, max_reps=7):
     """wick's CPU attention (the oracle) on the host: decode over all 24 layers, median of reps."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -125,6 +143,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--pmc-case", action="store_true",
+                    help="short fixed workload for rocprofv3 --pmc runs: 24 decode launches (one per layer) and a "
+                         "256 MiB device copy that calibrates the byte counters")
     ap.add_argument("--decode-chunk", type=int, default=0)
     ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph)")
     args = ap.parse_args()
@@ -145,6 +166,9 @@ def main():
 
     # ---------------- decode (the headline)
     kv, q, att = setup_decode(torch, DeviceKvCache, dev)
+    if args.pmc_case:
+        pmc_case(torch, kv, q, att, dev)
+        return
     if args.decode_chunk:
         kv.set_option(_native.OPT_DECODE_CHUNK, args.decode_chunk)
     hd, qd = c["heads"] * c["d"], c["heads"] * c["d"]
@@ -169,6 +193,13 @@ def main():
         ms_step, ms_launch = time_launches(torch, graph.replay, c["layers"], args.steps, args.warmup)
         mode = "hip-graph"
     grid = kv.last_grid()
+    # HBM bytes per launch measured by the committed rocprofv3 --pmc runs on this
+    # same workload (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size).
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "pmc_traffic_decode64_qwen25_32k.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("traffic_bytes_per_launch")
     bytes_layer = decode_bytes(c["L"], c["heads"], c["kv_heads"], c["d"])
     bytes_step = bytes_layer * c["layers"]
     value = bytes_step / (ms_step * 1e-3) / 1e9
@@ -194,7 +225,7 @@ def main():
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "kernel": "wick::decode_kernel<64>", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_launch": bytes_layer, "us_per_launch": round(ms_launch * 1e3, 3)},
+                     "traffic": traffic, "bytes_per_launch": bytes_layer, "us_per_launch": round(ms_launch * 1e3, 3)},
     }
 
     # ---------------- prefill (configs[2], T = 2048)

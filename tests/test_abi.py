@@ -55,3 +55,30 @@ def test_no_device_is_an_error_not_a_fallback():
     rc = lib.wick_hip_kv_create(1, 16, 2, 64, ctypes.byref(h))
     assert rc == _native.EDEVICE, rc
     assert not h.value
+
+
+def test_host_mirror_loads_and_reports_errors():
+    import numpy as np
+    from wick_amd import host
+    from wick_amd.model import Config
+    lib = host.load()
+    assert lib.wick_host_model_create(None, None, None, None, None, None, 1) is None
+    assert b"null" in lib.wick_host_last_error()
+    # a model can be built on the CPU; a device cache cannot be made without a GPU
+    cfg = Config("llama", 32, 64, 1, 4, 2, 16, 8, rms_eps=1e-5)
+    rng = np.random.default_rng(0)
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)  # noqa: E731
+    w = {"embed": f(8, 32), "norm": np.ones(32, np.float32), "lm_head": None,
+         "layers": [{"attn_norm": np.ones(32, np.float32), "wq": f(64, 32), "wk": f(32, 32), "wv": f(32, 32),
+                     "wo": f(32, 64), "bq": None, "bk": None, "bv": None, "q_norm": None, "k_norm": None,
+                     "ffn_norm": np.ones(32, np.float32), "w_gate": f(64, 32), "w_up": f(64, 32),
+                     "w_down": f(32, 64)}]}
+    m = host.HostModel(cfg, w, threads=2)
+    try:
+        import torch
+        if torch.cuda.device_count() > 0:
+            return
+    except ImportError:
+        pass
+    with pytest.raises(RuntimeError, match="no HIP device|wick_hip_kv_create"):
+        m.new_state(16)
