@@ -85,7 +85,6 @@ int wick_hip_kv_synchronize(wick_hip_kv *kv);
 /* Tuning knobs. */
 #define WICK_HIP_OPT_DECODE_CHUNK 1 /* positions per decode workgroup (multiple of 64; 0 = automatic) */
 #define WICK_HIP_OPT_PREFILL_PAIRING 2 /* 1 = pair causal row blocks (b, n-1-b); 0 = never; -1 = automatic */
-#define WICK_HIP_OPT_DECODE_MERGE 3 /* 0 = split-K partials merged inside the decode kernel (default); 1 = by a second kernel */
 int wick_hip_kv_set_option(wick_hip_kv *kv, int option, int value);
 
 /* Number of workgroups the last attention call launched (for measurement). */

@@ -68,28 +68,25 @@ def test_decode_lengths_and_head_dims(L, d):
     check(q, k, v, 1, L - 1, 9, 3, d)
 
 
-@pytest.mark.parametrize("merge", [0, 1])
 @pytest.mark.parametrize("chunk", [64, 128, 192, 256, 1024, 4096, 8192])
-def test_decode_chunk_sizes(chunk, merge):
-    # chunk counts from 1 (single workgroup) through one and two merge levels,
-    # with the in-kernel merge tree and with the separate merge kernel
+def test_decode_chunk_sizes(chunk):
+    # chunk counts from 1 (no merge pass) up to 128
     L = 8191
     q, k, v = make_inputs(11, 1, L - 1, 14, 2, 64)
-    check(q, k, v, 1, L - 1, 14, 2, 64,
-          options=[(_native.OPT_DECODE_CHUNK, chunk), (_native.OPT_DECODE_MERGE, merge)])
+    check(q, k, v, 1, L - 1, 14, 2, 64, options=[(_native.OPT_DECODE_CHUNK, chunk)])
 
 
-@pytest.mark.parametrize("merge", [0, 1])
 @pytest.mark.parametrize("d", [16, 32, 64, 128])
-def test_decode_merge_modes_agree(merge, d):
-    L = 5000
-    q, k, v = make_inputs(d + 100 * merge, 1, L - 1, 12, 3, d)
-    check(q, k, v, 1, L - 1, 12, 3, d, options=[(_native.OPT_DECODE_CHUNK, 64), (_native.OPT_DECODE_MERGE, merge)])
+def test_decode_many_chunks_all_head_dims(d):
+    # 256 chunks (the most one call uses) through the merge pass at every head_dim
+    L = 16384
+    q, k, v = make_inputs(d + 100, 1, L - 1, 12, 3, d)
+    check(q, k, v, 1, L - 1, 12, 3, d, options=[(_native.OPT_DECODE_CHUNK, 64)])
 
 
-def test_decode_repeated_launches_reuse_counters():
-    # the merge counters are reset by the kernel itself: many launches in a row
-    # on one handle, alternating layers, must all be right
+def test_decode_repeated_launches_reuse_workspace():
+    # the split-K workspace is shared by every call on a handle: many launches
+    # in a row, alternating layers, must all be right
     L = 6000
     with DeviceKvCache(2, L, 2, 64) as kv:
         kv.set_option(_native.OPT_DECODE_CHUNK, 64)

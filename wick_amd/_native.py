@@ -18,7 +18,6 @@ EDEVICE = -4
 
 OPT_DECODE_CHUNK = 1
 OPT_PREFILL_PAIRING = 2
-OPT_DECODE_MERGE = 3
 
 # Every symbol include/wick_hip.h declares, with its ctypes signature.
 _P = ctypes.c_void_p

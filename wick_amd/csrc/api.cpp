@@ -51,12 +51,11 @@ struct wick_hip_kv {
     // staging for the host-pointer entry points
     float *q_dev = nullptr, *att_dev = nullptr, *kst_dev = nullptr, *vst_dev = nullptr;
     size_t q_cap = 0, att_cap = 0, kst_cap = 0;
-    // decode split-K workspace
+    // decode split-K workspace (partial softmax states of the chunks)
     float *part = nullptr;
-    int *counters = nullptr;
     int ws_units = 0;
     // options
-    int decode_chunk = 0, pairing = -1, decode_merge = 0, last_grid = 0;
+    int decode_chunk = 0, pairing = -1, last_grid = 0;
     int decode_blocks_per_cu = 1;
 
     size_t layer_floats() const { return (size_t)kv_heads * capacity * head_dim; }
@@ -77,19 +76,14 @@ int grow(float **buf, size_t *cap, size_t need, const char *what) {
     return WICK_HIP_OK;
 }
 
-// Decode workspace for `units` (kv head, 16-head slice) pairs; counters start
-// at zero and every launch leaves them at zero.
+// Decode workspace for `units` (kv head, 16-head slice) pairs.  Grown on
+// demand; a decode launch rewrites every state it later reads.
 int ensure_workspace(wick_hip_kv *kv, int units) {
     if (units <= kv->ws_units) return WICK_HIP_OK;
     if (kv->part) (void)hipFree(kv->part);
-    if (kv->counters) (void)hipFree(kv->counters);
     kv->part = nullptr;
-    kv->counters = nullptr;
     kv->ws_units = 0;
     HIP_TRY(hipMalloc(&kv->part, wick::decode_workspace_floats(units, kv->head_dim) * sizeof(float)));
-    const size_t ncnt = (size_t)units * (wick::kDecodeFan + 1);
-    HIP_TRY(hipMalloc(&kv->counters, ncnt * sizeof(int)));
-    HIP_TRY(hipMemsetAsync(kv->counters, 0, ncnt * sizeof(int), kv->stream));
     kv->ws_units = units;
     return WICK_HIP_OK;
 }
@@ -139,7 +133,6 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
         a.v = kv->v_layer(layer);
         a.att = att_dev;
         a.part = kv->part;
-        a.counters = kv->counters;
         a.capacity = kv->capacity;
         a.len = len;
         a.kv_heads = kv->kv_heads;
@@ -147,8 +140,6 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
         a.hslices = hslices;
         a.chunk = chunk;
         a.nchunks = nchunks;
-        a.ngroups = (nchunks + wick::kDecodeFan - 1) / wick::kDecodeFan;
-        a.merge_mode = kv->decode_merge;
         a.scale = scale;
         const int grid = units * nchunks;
         kv->last_grid = grid;
@@ -240,7 +231,6 @@ void wick_hip_kv_destroy(wick_hip_kv *kv) {
     float *bufs[] = {kv->k, kv->v, kv->q_dev, kv->att_dev, kv->kst_dev, kv->vst_dev, kv->part};
     for (float *b : bufs)
         if (b) (void)hipFree(b);
-    if (kv->counters) (void)hipFree(kv->counters);
     if (kv->own_stream) (void)hipStreamDestroy(kv->own_stream);
     delete kv;
 }
@@ -267,10 +257,6 @@ int wick_hip_kv_set_option(wick_hip_kv *kv, int option, int value) {
     case WICK_HIP_OPT_PREFILL_PAIRING:
         if (value < -1 || value > 1) return fail(WICK_HIP_EINVAL, "pairing must be -1, 0 or 1");
         kv->pairing = value;
-        return WICK_HIP_OK;
-    case WICK_HIP_OPT_DECODE_MERGE:
-        if (value < 0 || value > 1) return fail(WICK_HIP_EINVAL, "decode merge must be 0 or 1");
-        kv->decode_merge = value;
         return WICK_HIP_OK;
     default:
         return fail(WICK_HIP_EINVAL, "unknown option %d", option);

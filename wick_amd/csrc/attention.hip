@@ -243,130 +243,40 @@ __device__ __forceinline__ void init_state(WaveState<D> &st) {
 
 // ------------------------------------------------------------------ decode
 
-// Workspace layout (floats), independent of the per-call chunk count; each
-// (unit, column) owns a contiguous run of child states, so a merge reads one
-// contiguous block:
-//   O0 [units][16 cols][256 chunks][D], m0 [units][16][256], l0 [units][16][256],
-//   O1 [units][16 cols][16 groups][D],  m1 [units][16][16],  l1 [units][16][16]
+// Partial states of the split-K decode, per (unit, column): O [units][16][256][D],
+// m and l [units][16][256] (unit = kv head x 16-head slice, column = query head
+// of the slice, 256 = most chunks per call).  The chunk states of a column are
+// contiguous, so the merge reads one contiguous block per column.
 size_t decode_workspace_floats(int units, int head_dim) {
-    return (size_t)units * ((size_t)kDecodeMaxChunks * 16 * (head_dim + 2) + (size_t)kDecodeFan * 16 * (head_dim + 2));
+    return (size_t)units * 16 * kDecodeMaxChunks * (head_dim + 2);
 }
-
-// A set of partial (O, m, l) states: state (child ch, column col) lives at
-// o[(col*cs + ch)*D ..], m[col*cs + ch], l[col*cs + ch].
-struct PView {
-    float *o, *m, *l;
-    int cs;
-};
 
 template <int D>
 struct DecodeSpace {
-    PView p0, p1;  // per-chunk states and per-group states, both for unit 0
+    float *o, *m, *l;
     __device__ DecodeSpace(float *part, int units) {
-        const size_t U = (size_t)units;
-        p0.o = part;
-        p0.m = p0.o + U * 16 * kDecodeMaxChunks * D;
-        p0.l = p0.m + U * 16 * kDecodeMaxChunks;
-        p0.cs = kDecodeMaxChunks;
-        p1.o = p0.l + U * 16 * kDecodeMaxChunks;
-        p1.m = p1.o + U * 16 * kDecodeFan * D;
-        p1.l = p1.m + U * 16 * kDecodeFan;
-        p1.cs = kDecodeFan;
+        o = part;
+        m = o + (size_t)units * 16 * kDecodeMaxChunks * D;
+        l = m + (size_t)units * 16 * kDecodeMaxChunks;
     }
-    // The states of `unit`, starting at child `first`.
-    __device__ static PView at(const PView &p, int unit, int first) {
-        const size_t base = (size_t)unit * 16 * p.cs + first;
-        return PView{p.o + base * D, p.m + base, p.l + base, p.cs};
+    // index of (unit, column, chunk) in m / l; times D for o
+    __device__ static size_t at(int unit, int col, int chunk) {
+        return ((size_t)unit * 16 + col) * kDecodeMaxChunks + chunk;
     }
 };
-
-// Device-scope (sc1) stores and loads: they bypass the caches that are not
-// coherent across the chip's XCDs, so a state stored by one workgroup and
-// loaded by another after a counter handshake needs no L2 writeback or
-// invalidate (both of which a release/acquire fence would issue per wave).
-__device__ __forceinline__ void st_dev(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_dev(const float *p) {
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Wait until this wave's device-scope stores have completed (are visible to
-// every CU), then take a ticket from *cnt once the whole workgroup has done so.
-// This is the release sequence the AMDGPU memory model uses for atomic stores,
-// without the L2 writeback that only non-atomic stores need.
-__device__ __forceinline__ int publish_and_count(int *cnt, int &ticket_smem) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) ticket_smem = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    return ticket_smem;
-}
-
-// Merge n <= 16 child states of one unit (view c) in child order, either into
-// one state stored with device-scope stores (view out) or -- when att != NULL --
-// into the normalised output att[(head0 + col)*D + d].  All child loads are
-// issued together.  Fixed order: the result does not depend on which
-// workgroup runs the merge.
-template <int D>
-__device__ void merge_children(const PView &c, int n, int ncols, const PView &out, float *att, int head0,
-                               float (&sw)[16][kDecodeFan], float (&sml)[2][16][kDecodeFan]) {
-    const int tid = threadIdx.x;
-    if (tid < 16 * kDecodeFan) {
-        const int col = tid / kDecodeFan, ch = tid % kDecodeFan;
-        const bool live = ch < n && col < ncols;
-        sml[0][col][ch] = live ? ld_dev(c.m + col * c.cs + ch) : -INFINITY;
-        sml[1][col][ch] = live ? ld_dev(c.l + col * c.cs + ch) : 0.f;
-    }
-    float v[kDecodeFan];
-    const int idx0 = tid;  // first (col, d) of this thread; ncols*D <= 2048 = 8 * 256
-    __syncthreads();
-    if (tid < 16) {
-        float M = -INFINITY;
-#pragma unroll
-        for (int ch = 0; ch < kDecodeFan; ch++) M = fmaxf(M, sml[0][tid][ch]);
-        const float Mref = (M == -INFINITY) ? 0.f : M;
-        float L = 0.f;
-#pragma unroll
-        for (int ch = 0; ch < kDecodeFan; ch++) {
-            const float e = exp2_fast((sml[0][tid][ch] - Mref) * kLog2e);
-            sw[tid][ch] = e;
-            L += sml[1][tid][ch] * e;
-        }
-        if (!att && tid < ncols) {
-            st_dev(out.m + tid * out.cs, M);
-            st_dev(out.l + tid * out.cs, L);
-        }
-        sml[1][tid][0] = L;  // total, read below for normalisation
-    }
-    __syncthreads();
-    for (int idx = idx0; idx < ncols * D; idx += blockDim.x) {
-        const int col = idx / D, d = idx % D;
-#pragma unroll
-        for (int ch = 0; ch < kDecodeFan; ch++) v[ch] = ch < n ? ld_dev(c.o + ((size_t)col * c.cs + ch) * D + d) : 0.f;
-        float o = 0.f;
-#pragma unroll
-        for (int ch = 0; ch < kDecodeFan; ch++) o += v[ch] * sw[col][ch];
-        if (att) att[(size_t)(head0 + col) * D + d] = o / sml[1][col][0];
-        else st_dev(out.o + (size_t)col * out.cs * D + d, o);
-    }
-}
 
 // One token (t = 1) over len cached positions, split-K: workgroup
 // (unit, chunk) runs 4 waves over positions chunk*C .. +C of one kv head for
 // up to 16 of its query heads (unit = kv head x 16-head slice), so every K/V
-// byte is read once for the whole GQA group.  Partial (max, sum, O) states are
-// merged by log-sum-exp, either by decode_merge_kernel (merge_mode 1) or in a
-// fixed-order tree of fan-in 16 inside this kernel (merge_mode 0), whose
-// last-arriving workgroup at each level does the merge and resets the level's
-// counter (so no memset is needed between launches).
+// byte is read once for the whole GQA group.  With one chunk the output is
+// written directly; otherwise the chunk's (max, sum, O) state per query head
+// goes to the workspace and decode_merge_kernel, the next launch on the
+// stream, combines them (the kernel boundary orders the two).
 template <int D>
 __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     using S = Shape<D>;
     __shared__ float sm_m[4][16], sm_l[4][16];
     __shared__ float sm_o[4][16][D];
-    __shared__ float sm_w[16][kDecodeFan], sm_ml[2][16][kDecodeFan];
-    __shared__ int s_ticket;
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int units = a.kv_heads * a.hslices;
@@ -400,8 +310,6 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     // Merge the 4 waves of this workgroup.  Wave 0 always holds the chunk's
     // first key, so the merged max is finite.
     const DecodeSpace<D> ws(a.part, units);
-    const PView mine = DecodeSpace<D>::at(ws.p0, unit, chunk);
-    const bool in_kernel = a.merge_mode == 0;
     for (int idx = threadIdx.x; idx < ncols * D; idx += blockDim.x) {
         const int c = idx / D, d = idx % D;
         float M = -INFINITY;
@@ -416,87 +324,60 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
         }
         if (a.nchunks == 1) {
             a.att[(size_t)(head0 + c) * D + d] = o / L;
-        } else if (in_kernel) {
-            st_dev(mine.o + (size_t)c * mine.cs * D + d, o);
-            if (d == 0) {
-                st_dev(mine.m + c * mine.cs, M);
-                st_dev(mine.l + c * mine.cs, L);
-            }
         } else {
-            mine.o[(size_t)c * mine.cs * D + d] = o;
+            const size_t s = DecodeSpace<D>::at(unit, c, chunk);
+            ws.o[s * D + d] = o;
             if (d == 0) {
-                mine.m[c * mine.cs] = M;
-                mine.l[c * mine.cs] = L;
+                ws.m[s] = M;
+                ws.l[s] = L;
             }
         }
     }
-    if (a.nchunks == 1 || !in_kernel) return;
-
-    // Level 1: the last of the (up to) 16 chunks of a group merges the group.
-    const int grp = chunk / kDecodeFan, gfirst = grp * kDecodeFan;
-    const int nin = min(kDecodeFan, a.nchunks - gfirst);
-    int *cnt1 = a.counters + (size_t)unit * (kDecodeFan + 1) + grp;
-    int *cnt2 = a.counters + (size_t)unit * (kDecodeFan + 1) + kDecodeFan;
-    if (publish_and_count(cnt1, s_ticket) != nin - 1) return;
-    if (threadIdx.x == 0) __hip_atomic_store(cnt1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-
-    const PView child = DecodeSpace<D>::at(ws.p0, unit, gfirst);
-    if (a.ngroups == 1) {
-        merge_children<D>(child, nin, ncols, PView{}, a.att, head0, sm_w, sm_ml);
-        return;
-    }
-    merge_children<D>(child, nin, ncols, DecodeSpace<D>::at(ws.p1, unit, grp), nullptr, head0, sm_w, sm_ml);
-
-    // Level 2: the last group merger of this unit writes the output.
-    if (publish_and_count(cnt2, s_ticket) != a.ngroups - 1) return;
-    if (threadIdx.x == 0) __hip_atomic_store(cnt2, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_children<D>(DecodeSpace<D>::at(ws.p1, unit, 0), a.ngroups, ncols, PView{}, a.att, head0, sm_w, sm_ml);
 }
 
-// Separate merge pass (merge_mode 1): workgroup (unit, col) merges the
-// nchunks (<= 256) partial states of one query head in chunk order; they are
-// contiguous in the workspace.  Thread (grp, d) of 256/D groups owns children
-// grp, grp + 256/D, ...; all of its O loads and the (m, l) loads (one child per
-// thread) are issued before any is used, so the pass costs one memory round
-// trip.  Per-thread sums run in child order and the group sums are combined
-// in group order: deterministic for a given nchunks.
+// Merge pass: workgroup (unit, column, 16-dim slice) combines the nchunks
+// (<= 256) partial states of one query head for 16 of its head dims.  Thread
+// (grp, dd) of 16 groups owns children grp, grp + 16, ...; all of its O loads
+// and the (m, l) loads (one child per thread) are issued before any is used,
+// so the pass costs one memory round trip.  Per-thread sums run in child
+// order and the group sums are combined in group order: deterministic for a
+// given nchunks.
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
-    constexpr int G = 256 / D;                  // thread groups over children
-    constexpr int NU = kDecodeMaxChunks / G;    // children per thread at most
+    constexpr int DW = 16;                        // head dims per workgroup
+    constexpr int NS = D / DW;                    // slices per column
+    constexpr int G = 256 / DW;                   // thread groups over children
+    constexpr int NB = kDecodeMaxChunks / G;      // children per thread
     __shared__ float sw[kDecodeMaxChunks];
     __shared__ float red[4];
-    __shared__ float so[G][D];
+    __shared__ float so[G][DW];
     const int units = a.kv_heads * a.hslices;
-    const int unit = blockIdx.x / 16, col = blockIdx.x % 16;
+    const int ds = blockIdx.x % NS, col = (blockIdx.x / NS) % 16, unit = blockIdx.x / (NS * 16);
     const int kvh = unit / a.hslices, slice = unit % a.hslices;
     const int col0 = slice * 16, ncols = min(16, a.group - col0);
     if (col >= ncols) return;
-    const int head = kvh * a.group + col0 + col;
     const DecodeSpace<D> ws(a.part, units);
-    const PView c = DecodeSpace<D>::at(ws.p0, unit, 0);
-    const float *co = c.o + (size_t)col * c.cs * D;
-    const float *cm = c.m + col * c.cs;
-    const float *cl = c.l + col * c.cs;
+    const size_t base = DecodeSpace<D>::at(unit, col, 0);
+    const float *o = ws.o + base * D + ds * DW, *m = ws.m + base, *l = ws.l + base;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int grp = tid / DW, dd = tid % DW;
     const int n = a.nchunks;
-    const int grp = tid / D, d = tid % D;
 
-    float v[NU];
+    float v[NB];
 #pragma unroll
-    for (int u = 0; u < NU; u++) {
+    for (int u = 0; u < NB; u++) {
         const int ch = grp + u * G;
-        v[u] = ch < n ? co[(size_t)ch * D + d] : 0.f;
+        v[u] = ch < n ? o[(size_t)ch * D + dd] : 0.f;
     }
-    const float mv = tid < n ? cm[tid] : -INFINITY;
-    const float lv = tid < n ? cl[tid] : 0.f;
+    const float mv = tid < n ? m[tid] : -INFINITY;
+    const float lv = tid < n ? l[tid] : 0.f;
     float M = mv;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
     if (lane == 0) red[w] = M;
     __syncthreads();
     M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float e = exp2_fast((mv - M) * kLog2e);
+    const float e = exp2_fast((mv - M) * kLog2e);  // 0 for absent children
     sw[tid] = e;
     float L = lv * e;
 #pragma unroll
@@ -506,19 +387,18 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
     __syncthreads();
     L = (red[0] + red[1]) + (red[2] + red[3]);
 
-    float o = 0.f;
+    // Branch-free: absent children have v = 0 and weight 0, so the weight
+    // reads are issued together instead of one LDS round trip per child.
+    float acc = 0.f;
 #pragma unroll
-    for (int u = 0; u < NU; u++) {
-        const int ch = grp + u * G;
-        if (ch < n) o += v[u] * sw[ch];
-    }
-    so[grp][d] = o;
+    for (int u = 0; u < NB; u++) acc += v[u] * sw[grp + u * G];
+    so[grp][dd] = acc;
     __syncthreads();
-    if (tid < D) {
-        float acc = 0.f;
+    if (tid < DW) {
+        float s = 0.f;
 #pragma unroll
-        for (int gg = 0; gg < G; gg++) acc += so[gg][tid];
-        a.att[(size_t)head * D + tid] = acc / L;
+        for (int gg = 0; gg < G; gg++) s += so[gg][tid];
+        a.att[(size_t)(kvh * a.group + col0 + col) * D + ds * DW + tid] = s / L;
     }
 }
 
@@ -623,9 +503,10 @@ int decode_blocks_per_cu(int head_dim) {
 hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_t s) {
     WICK_DISPATCH_D(head_dim, decode_kernel, dim3(grid), dim3(256), 0, s, a);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.nchunks == 1 || a.merge_mode != 1) return e;
+    if (e != hipSuccess || a.nchunks == 1) return e;
     const int units = a.kv_heads * a.hslices;
-    WICK_DISPATCH_D(head_dim, decode_merge_kernel, dim3(units * 16), dim3(256), 0, s, a);
+    const int slices = head_dim / 16;
+    WICK_DISPATCH_D(head_dim, decode_merge_kernel, dim3(units * 16 * slices), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -7,11 +7,8 @@
 
 namespace wick {
 
-// Decode workgroups merge their partial softmax states in a tree of fan-in
-// kDecodeFan (two levels at most), so one call handles at most
-// kDecodeFan * kDecodeFan chunks per (kv head, head slice).
-constexpr int kDecodeFan = 16;
-constexpr int kDecodeMaxChunks = kDecodeFan * kDecodeFan;
+// Most split-K chunks one decode call uses per (kv head, 16-head slice).
+constexpr int kDecodeMaxChunks = 256;
 constexpr int kTileRows = 16;  // query rows (or heads) per MFMA column block
 
 struct DecodeArgs {
@@ -20,9 +17,7 @@ struct DecodeArgs {
     const float *v;
     float *att;       // [heads*D]
     float *part;      // partial states, see decode_workspace_floats
-    int *counters;    // [units][kDecodeFan + 1], zero between launches
-    int capacity, len, kv_heads, group, hslices, chunk, nchunks, ngroups;
-    int merge_mode;   // 0: in-kernel merge tree, 1: separate merge kernel
+    int capacity, len, kv_heads, group, hslices, chunk, nchunks;
     float scale;
 };
 
@@ -47,6 +42,7 @@ size_t decode_workspace_floats(int units, int head_dim);
 // Decode workgroups one CU holds at once (from the kernel's register and LDS use).
 int decode_blocks_per_cu(int head_dim);
 
+// Launches decode_kernel and, when it splits the keys, decode_merge_kernel.
 hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_t s);
 hipError_t launch_prefill(int head_dim, const PrefillArgs &a, int grid, hipStream_t s);
 hipError_t launch_append(int head_dim, const AppendArgs &a, hipStream_t s);
