@@ -84,7 +84,8 @@ int wick_hip_kv_synchronize(wick_hip_kv *kv);
 
 /* Tuning knobs. */
 #define WICK_HIP_OPT_DECODE_CHUNK 1 /* positions per decode workgroup (multiple of 64; 0 = automatic) */
-#define WICK_HIP_OPT_PREFILL_PAIRING 2 /* 1 = pair causal row blocks (b, n-1-b); 0 = never; -1 = automatic */
+#define WICK_HIP_OPT_PREFILL_PAIRING 2 /* one-wave-per-block prefill: 1 = pair row blocks (b, n-1-b); 0 = never; -1 = automatic */
+#define WICK_HIP_OPT_PREFILL_SPLIT 3   /* 1 = workgroup per row block, keys split across its 4 waves (default); 0 = one wave per block */
 int wick_hip_kv_set_option(wick_hip_kv *kv, int option, int value);
 
 /* Number of workgroups the last attention call launched (for measurement). */

@@ -167,12 +167,21 @@ def test_prefill_ragged(t, start, d):
     check(q, k, v, t, start, 4, 2, d)
 
 
-@pytest.mark.parametrize("pairing", [0, 1])
+@pytest.mark.parametrize("split,pairing", [(0, 0), (0, 1), (1, -1)])
 @pytest.mark.parametrize("heads,kv_heads", [(9, 3), (14, 2), (32, 4), (6, 6)])
-def test_prefill_pairing_and_groups(pairing, heads, kv_heads):
+def test_prefill_schedules_and_groups(split, pairing, heads, kv_heads):
     t, start = 300, 20
     q, k, v = make_inputs(heads + pairing, t, start, heads, kv_heads, 64)
-    check(q, k, v, t, start, heads, kv_heads, 64, options=[(_native.OPT_PREFILL_PAIRING, pairing)])
+    check(q, k, v, t, start, heads, kv_heads, 64,
+          options=[(_native.OPT_PREFILL_SPLIT, split), (_native.OPT_PREFILL_PAIRING, pairing)])
+
+
+@pytest.mark.parametrize("split", [0, 1])
+@pytest.mark.parametrize("d", [16, 32, 64, 128])
+def test_prefill_schedules_agree_within_tolerance(split, d):
+    t, start = 77, 200
+    q, k, v = make_inputs(d * 3 + split, t, start, 8, 2, d)
+    check(q, k, v, t, start, 8, 2, d, options=[(_native.OPT_PREFILL_SPLIT, split)])
 
 
 def test_prefill_bit_stable():

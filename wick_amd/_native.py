@@ -18,6 +18,7 @@ EDEVICE = -4
 
 OPT_DECODE_CHUNK = 1
 OPT_PREFILL_PAIRING = 2
+OPT_PREFILL_SPLIT = 3
 
 # Every symbol include/wick_hip.h declares, with its ctypes signature.
 _P = ctypes.c_void_p

@@ -55,7 +55,7 @@ struct wick_hip_kv {
     float *part = nullptr;
     int ws_units = 0;
     // options
-    int decode_chunk = 0, pairing = -1, last_grid = 0;
+    int decode_chunk = 0, pairing = -1, prefill_split = 1, last_grid = 0;
     int decode_blocks_per_cu = 1;
 
     size_t layer_floats() const { return (size_t)kv_heads * capacity * head_dim; }
@@ -168,10 +168,10 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
     }
     a.paired = paired;
     a.items = paired ? (a.nblocks + 1) / 2 : a.nblocks;
+    a.split = kv->prefill_split;
     a.scale = scale;
-    const int grid = kv->kv_heads * ((a.items + 3) / 4);
-    kv->last_grid = grid;
-    hipError_t e = wick::launch_prefill(D, a, grid, kv->stream);
+    kv->last_grid = wick::prefill_grid(a);
+    hipError_t e = wick::launch_prefill(D, a, kv->stream);
     if (e != hipSuccess) return hip_fail(e, "prefill kernel launch");
     return WICK_HIP_OK;
 }
@@ -257,6 +257,10 @@ int wick_hip_kv_set_option(wick_hip_kv *kv, int option, int value) {
     case WICK_HIP_OPT_PREFILL_PAIRING:
         if (value < -1 || value > 1) return fail(WICK_HIP_EINVAL, "pairing must be -1, 0 or 1");
         kv->pairing = value;
+        return WICK_HIP_OK;
+    case WICK_HIP_OPT_PREFILL_SPLIT:
+        if (value < 0 || value > 1) return fail(WICK_HIP_EINVAL, "prefill split must be 0 or 1");
+        kv->prefill_split = value;
         return WICK_HIP_OK;
     default:
         return fail(WICK_HIP_EINVAL, "unknown option %d", option);

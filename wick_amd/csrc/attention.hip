@@ -455,6 +455,71 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
     }
 }
 
+// Workgroup = one 16-row block b of one kv head; its causal key range
+// 0 .. start + last token of the block is split into 4 contiguous tile ranges,
+// one per wave, whose states are merged through LDS.  Blocks are dispatched
+// heaviest first (largest b), so the many workgroups of a causal launch
+// balance across CUs without pairing, and every SIMD holds several waves
+// (single-buffered tiles at head_dim 128 leave room for three) to overlap one
+// wave's softmax with another's MFMAs.  The wave holding key 0 -- valid for
+// every row -- keeps each merged max finite.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_split_kernel(const PrefillArgs a) {
+    using S = Shape<D>;
+    __shared__ float sm_m[4][16], sm_l[4][16];
+    __shared__ float sm_o[4][16][D];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int kvh = blockIdx.x % a.kv_heads;
+    const int b = a.nblocks - 1 - (int)(blockIdx.x / a.kv_heads);
+    const float *Kh = a.k + (size_t)kvh * a.capacity * D;
+    const float *Vh = a.v + (size_t)kvh * a.capacity * D;
+    const int col = lane & 15, g = lane >> 4;
+    const int heads = a.kv_heads * a.group;
+    const int nrows = a.t * a.group;
+    const int r = 16 * b + col;
+    const bool valid = r < nrows;
+    const int i = valid ? r / a.group : 0, hh = valid ? r % a.group : 0;
+    const int lim = valid ? a.start + i + 1 : 1;
+    const int imax = min(16 * b + 15, nrows - 1) / a.group;
+    const int kend = a.start + imax + 1;
+    const int nt = (kend + 15) >> 4;
+    const int ks = 16 * ((w * nt) >> 2), ke = min(16 * (((w + 1) * nt) >> 2), kend);
+
+    f4 q[S::KJ];
+    load_q<D>(a.q + (size_t)i * heads * D + (size_t)(kvh * a.group + hh) * D, a.q, valid, lane, q);
+    WaveState<D> st;
+    init_state<D>(st);
+    attend_range<D, (D < 128)>(Kh, Vh, ks, ke, 0, S::TG, lim, a.scale, q, lane, st);
+    st.l = col_sum(st.l);
+    if (g == 0) {
+        sm_m[w][col] = st.m;
+        sm_l[w][col] = st.l;
+    }
+#pragma unroll
+    for (int db = 0; db < S::DB; db++)
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) sm_o[w][col][out_dim<D>(g, rr, db)] = st.o[db][rr];
+    __syncthreads();
+
+    for (int idx = threadIdx.x; idx < 16 * D; idx += blockDim.x) {
+        const int c = idx / D, d = idx % D;
+        const int rc = 16 * b + c;
+        if (rc >= nrows) break;  // rows beyond the chunk are padding
+        float M = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) M = fmaxf(M, sm_m[ww][c]);
+        float o = 0.f, L = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) {
+            const float e = exp2_fast((sm_m[ww][c] - M) * kLog2e);
+            o += sm_o[ww][c][d] * e;
+            L += sm_l[ww][c] * e;
+        }
+        const int ic = rc / a.group, hc = rc % a.group;
+        a.att[(size_t)ic * heads * D + (size_t)(kvh * a.group + hc) * D + d] = o / L;
+    }
+}
+
 // ------------------------------------------------------------------ append
 
 // src rows [t][kv_heads*D] -> cache [kv_heads][capacity][D] at start.. (the
@@ -510,8 +575,17 @@ hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(int head_dim, const PrefillArgs &a, int grid, hipStream_t s) {
-    WICK_DISPATCH_D(head_dim, prefill_kernel, dim3(grid), dim3(256), 0, s, a);
+int prefill_grid(const PrefillArgs &a) {
+    return a.split ? a.kv_heads * a.nblocks : a.kv_heads * ((a.items + 3) / 4);
+}
+
+hipError_t launch_prefill(int head_dim, const PrefillArgs &a, hipStream_t s) {
+    const int grid = prefill_grid(a);
+    if (a.split) {
+        WICK_DISPATCH_D(head_dim, prefill_split_kernel, dim3(grid), dim3(256), 0, s, a);
+    } else {
+        WICK_DISPATCH_D(head_dim, prefill_kernel, dim3(grid), dim3(256), 0, s, a);
+    }
     return hipGetLastError();
 }
 

@@ -27,6 +27,7 @@ struct PrefillArgs {
     const float *v;
     float *att;       // [t][heads*D]
     int capacity, t, start, kv_heads, group, nblocks, items, paired;
+    int split;        // 1: prefill_split_kernel (4-way key split per workgroup)
     float scale;
 };
 
@@ -44,7 +45,8 @@ int decode_blocks_per_cu(int head_dim);
 
 // Launches decode_kernel and, when it splits the keys, decode_merge_kernel.
 hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_t s);
-hipError_t launch_prefill(int head_dim, const PrefillArgs &a, int grid, hipStream_t s);
+int prefill_grid(const PrefillArgs &a);
+hipError_t launch_prefill(int head_dim, const PrefillArgs &a, hipStream_t s);
 hipError_t launch_append(int head_dim, const AppendArgs &a, hipStream_t s);
 
 }  // namespace wick
