@@ -10,8 +10,10 @@ the 256 MB Infinity Cache).  Inputs are resident in HBM before timing starts.
 
 value  = algorithmic bytes per step / step time, in GB/s, where one layer
          reads 4*(2*L*Hkv*d + 2*Hq*d) bytes (K, V, q, and writes att).
-Also reported: causal prefill TFLOP/s (configs[2], Qwen3 shape, T = 2048) and
-the CPU oracle timed on the host cores on a bounded sample (cpu_baseline).
+Also reported: causal prefill TFLOP/s (configs[2], Qwen3 shape, T = 512 and
+2048), chunked prefill, long-context decode with a split-K chunk
+sweep, e2e decode tok/s and the CPU oracle timed on
+the host cores on a bounded sample (cpu_baseline).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -135,6 +137,81 @@ def cpu_baseline_decode(kv, q_host, threads, budget_s=12.0, max_reps=7):
     return step_s, len(times)
 
 
+CHUNKED = dict(heads=32, kv_heads=4, d=64, t=512, start=1536, theta=10000.0, seed=4)
+LONG = dict(heads=32, kv_heads=8, d=128, layers=32, L=65536, theta=500000.0, seed=5)
+
+
+def measure_prefill(torch, kv_cls, dev, heads, kv_heads, d, T, start, theta, seed, qk_norm, steps):
+    """One layer's attention over T new tokens after `start` cached positions; returns (us, flops)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    inv = inv_freq_torch(theta, d, dev)
+    L = start + T
+
+    def norm(x, h):
+        if not qk_norm:
+            return x
+        x = x.view(-1, h, d)
+        return (x * torch.rsqrt((x * x).mean(-1, keepdim=True) + 1e-6)).view(-1, h * d)
+    q = rope_torch(norm(torch.randn(T, heads * d, generator=g, device=dev), heads), heads, d,
+                   torch.arange(start, L, device=dev), inv).contiguous()
+    k = rope_torch(norm(torch.randn(L, kv_heads * d, generator=g, device=dev), kv_heads), kv_heads, d,
+                   torch.arange(L, device=dev), inv).contiguous()
+    v = torch.randn(L, kv_heads * d, generator=g, device=dev)
+    att = torch.empty_like(q)
+    kv = kv_cls(1, L, kv_heads, d)
+    kv.set_stream(torch.cuda.current_stream().cuda_stream)
+    kv.append_device(0, 0, L, k.data_ptr(), v.data_ptr())
+
+    def step():
+        kv.attention_device(0, heads, q.data_ptr(), T, start, att.data_ptr())
+    ms, _ = time_launches(torch, step, 1, steps, 2)
+    kv.close()
+    return ms * 1e3, prefill_flops(T, heads, d, start)
+
+
+def measure_long_decode(torch, kv_cls, native, dev, steps):
+    """32 layers x 65536 positions (16 GiB of K+V), one token per layer per step."""
+    c = LONG
+    g = torch.Generator(device=dev)
+    g.manual_seed(c["seed"])
+    inv = inv_freq_torch(c["theta"], c["d"], dev)
+    kv = kv_cls(c["layers"], c["L"], c["kv_heads"], c["d"])
+    kv.set_stream(torch.cuda.current_stream().cuda_stream)
+    pos = torch.arange(c["L"], device=dev)
+    for layer in range(c["layers"]):
+        k = rope_torch(torch.randn(c["L"], c["kv_heads"] * c["d"], generator=g, device=dev), c["kv_heads"], c["d"],
+                       pos, inv).contiguous()
+        v = torch.randn(c["L"], c["kv_heads"] * c["d"], generator=g, device=dev)
+        kv.append_device(layer, 0, c["L"], k.data_ptr(), v.data_ptr())
+        torch.cuda.synchronize()
+        del k, v
+    hd = c["heads"] * c["d"]
+    q = rope_torch(torch.randn(c["layers"], hd, generator=g, device=dev), c["heads"], c["d"],
+                   torch.full((c["layers"],), c["L"] - 1, device=dev), inv).contiguous()
+    att = torch.empty_like(q)
+
+    def step():
+        for layer in range(c["layers"]):
+            kv.attention_device(layer, c["heads"], q.data_ptr() + 4 * hd * layer, 1, c["L"] - 1,
+                                att.data_ptr() + 4 * hd * layer)
+    bytes_layer = decode_bytes(c["L"], c["heads"], c["kv_heads"], c["d"])
+    sweep = []
+    for chunk in (0, 512, 1024, 2048, 4096, 8192):
+        kv.set_option(native.OPT_DECODE_CHUNK, chunk)
+        _, ms_launch = time_launches(torch, step, c["layers"], steps, 2)
+        gbs = bytes_layer / (ms_launch * 1e-3) / 1e9
+        sweep.append({"chunk": chunk if chunk else "auto", "workgroups": kv.last_grid(),
+                      "us_per_layer": round(ms_launch * 1e3, 2), "GBps": round(gbs, 1),
+                      "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 1)})
+    kv.set_option(native.OPT_DECODE_CHUNK, 0)
+    kv.close()
+    best = sweep[0]
+    return {"workload": "Llama-3-8B shape (Hq 32 / Hkv 8, d 128), 32 layers x 65536 positions (16 GiB K+V), "
+                        "one query token per layer per step, eager launches",
+            "bytes_per_layer": bytes_layer, "auto": best, "chunk_sweep": sweep}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -143,6 +220,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--no-long", action="store_true", help="skip configs[4] (16 GiB long-context decode)")
     ap.add_argument("--pmc-case", action="store_true",
                     help="short fixed workload for rocprofv3 --pmc runs: 24 decode launches (one per layer) and a "
                          "256 MiB device copy that calibrates the byte counters")
@@ -223,47 +301,39 @@ def main():
                    "layers_per_step": c["layers"], "context": c["L"], "decode_workgroups": grid,
                    "launch": mode, "eager_ms_per_step": round(ms_step_eager, 4)},
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "kernel": "wick::decode_kernel<64>", "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": "wick::decode_kernel<64> + wick::decode_merge_kernel<64> (one call)", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "bytes_per_launch": bytes_layer, "us_per_launch": round(ms_launch * 1e3, 3)},
     }
 
-    # ---------------- prefill (configs[2], T = 2048)
+    # ---------------- prefill (configs[2] at T = 512 and 2048; configs[3] chunked)
     if not args.no_prefill:
-        p = PRE
-        g = torch.Generator(device=dev)
-        g.manual_seed(p["seed"])
-        inv = inv_freq_torch(p["theta"], p["d"], dev)
-        T = p["T"]
-
-        def qknorm(x, heads):
-            x = x.view(T, heads, p["d"])
-            return (x * torch.rsqrt((x * x).mean(-1, keepdim=True) + p["eps"])).view(T, heads * p["d"])
-        pos = torch.arange(T, device=dev)
-        pq = rope_torch(qknorm(torch.randn(T, p["heads"] * p["d"], generator=g, device=dev), p["heads"]),
-                        p["heads"], p["d"], pos, inv).contiguous()
-        pk = rope_torch(qknorm(torch.randn(T, p["kv_heads"] * p["d"], generator=g, device=dev), p["kv_heads"]),
-                        p["kv_heads"], p["d"], pos, inv).contiguous()
-        pv = torch.randn(T, p["kv_heads"] * p["d"], generator=g, device=dev)
-        patt = torch.empty_like(pq)
-        pkv = DeviceKvCache(1, T, p["kv_heads"], p["d"])
-        pkv.set_stream(torch.cuda.current_stream().cuda_stream)
-        pkv.append_device(0, 0, T, pk.data_ptr(), pv.data_ptr())
-
-        def pstep():
-            pkv.attention_device(0, p["heads"], pq.data_ptr(), T, 0, patt.data_ptr())
-        psteps = max(5, args.steps // 10)
-        ms_p, _ = time_launches(torch, pstep, 1, psteps, max(2, args.warmup // 5))
-        fl = prefill_flops(T, p["heads"], p["d"])
-        tf = fl / (ms_p * 1e-3) / 1e12
+        pre = {}
+        for T in (512, 2048):
+            pre[T] = measure_prefill(torch, DeviceKvCache, dev, PRE["heads"], PRE["kv_heads"], PRE["d"], T, 0,
+                                     PRE["theta"], PRE["seed"], qk_norm=True, steps=max(5, args.steps // 10))
+        us2048, fl2048 = pre[2048]
+        tf = fl2048 / (us2048 * 1e-6) / 1e12
         out["prefill_tflops"] = round(tf, 2)
-        out["roofline_prefill"] = {"bound": "mfma", "kernel": "wick::prefill_kernel<128>", "achieved": round(tf, 2),
-                                   "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+        out["roofline_prefill"] = {"bound": "mfma", "kernel": "wick::prefill_split_kernel<128>",
+                                   "achieved": round(tf, 2), "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                                    "frac": round(tf / F32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
-                                   "flops_per_launch": fl, "us_per_launch": round(ms_p * 1e3, 2),
+                                   "flops_per_launch": fl2048, "us_per_launch": round(us2048, 2),
                                    "workload": "causal prefill, Qwen3-0.6B shape (Hq 16 / Hkv 8, d 128), T 2048, "
                                                "QK-norm + RoPE applied, empty cache"}
-        pkv.close()
+        us512, fl512 = pre[512]
+        out["prefill_t512"] = {"us_per_launch": round(us512, 2), "tflops": round(fl512 / (us512 * 1e-6) / 1e12, 2)}
+        c4 = CHUNKED
+        us4, fl4 = measure_prefill(torch, DeviceKvCache, dev, c4["heads"], c4["kv_heads"], c4["d"], c4["t"],
+                                   c4["start"], c4["theta"], c4["seed"], qk_norm=False, steps=max(5, args.steps // 10))
+        out["chunked_prefill"] = {"workload": "TinyLlama-1.1B shape (Hq 32 / Hkv 4, d 64), 512 tokens appended "
+                                              "onto 1536 cached positions, per layer",
+                                  "us_per_layer": round(us4, 2), "tflops": round(fl4 / (us4 * 1e-6) / 1e12, 2),
+                                  "flops_per_layer": fl4}
+
+    # ---------------- long decode: Llama-3-8B shape, L = 65536, split-K chunk sweep
+    if not args.no_long:
+        out["long_decode"] = measure_long_decode(torch, DeviceKvCache, _native, dev, steps=max(4, args.steps // 20))
 
     # ---------------- e2e: wick's forward, attention on the GPU
     if not args.no_e2e:
