@@ -221,9 +221,10 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--no-long", action="store_true", help="skip configs[4] (16 GiB long-context decode)")
-    ap.add_argument("--pmc-case", action="store_true",
-                    help="short fixed workload for rocprofv3 --pmc runs: 24 decode launches (one per layer) and a "
-                         "256 MiB device copy that calibrates the byte counters")
+    ap.add_argument("--pmc-case", nargs="?", const="decode", choices=["decode", "prefill"],
+                    help="short fixed workload for rocprofv3 --pmc runs: 'decode' = 24 decode calls (one per layer) "
+                         "and a 256 MiB device copy that calibrates the byte counters; 'prefill' = 3 launches of "
+                         "configs[2] at T=2048")
     ap.add_argument("--decode-chunk", type=int, default=0)
     ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph)")
     args = ap.parse_args()
@@ -242,9 +243,15 @@ def main():
     torch.cuda.set_stream(stream)
     c = DEC
 
+    if args.pmc_case == "prefill":
+        measure_prefill(torch, DeviceKvCache, dev, PRE["heads"], PRE["kv_heads"], PRE["d"], PRE["T"], 0,
+                        PRE["theta"], PRE["seed"], qk_norm=True, steps=3)
+        print("pmc case done: prefill T=2048", flush=True)
+        return
+
     # ---------------- decode (the headline)
     kv, q, att = setup_decode(torch, DeviceKvCache, dev)
-    if args.pmc_case:
+    if args.pmc_case == "decode":
         pmc_case(torch, kv, q, att, dev)
         return
     if args.decode_chunk:

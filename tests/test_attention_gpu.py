@@ -222,3 +222,40 @@ def test_errors_are_reported():
             kv.append(0, 60, np.zeros((5, 128), np.float32), np.zeros((5, 128), np.float32))
         with pytest.raises(_native.WickHipError):
             kv.set_option(_native.OPT_DECODE_CHUNK, 100)
+
+
+def test_decode_hip_graph_replays_match_eager():
+    """bench.py replays decode calls captured in a HIP graph: every replay, with
+    eager work and synchronisations in between, must give the eager result bit
+    for bit (the graph holds no memset nodes)."""
+    import torch
+    L, heads, kvh, d, layers = 9000, 14, 2, 64, 3
+    dev = torch.device("cuda:0")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s), DeviceKvCache(layers, L, kvh, d) as kv:
+        kv.set_stream(s.cuda_stream)
+        qs = []
+        for layer in range(layers):
+            q, k, v = make_inputs(70 + layer, 1, L - 1, heads, kvh, d)
+            kv.append(layer, 0, k, v)
+            qs.append(q)
+        qd = torch.tensor(np.concatenate(qs), device=dev)
+        att = torch.zeros_like(qd)
+        hd = heads * d
+
+        def step():
+            for layer in range(layers):
+                kv.attention_device(layer, heads, qd.data_ptr() + 4 * hd * layer, 1, L - 1,
+                                    att.data_ptr() + 4 * hd * layer)
+        step()
+        s.synchronize()
+        eager = att.cpu().numpy().copy()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            step()
+        for it in range(4):
+            att.zero_()
+            g.replay()
+            s.synchronize()
+            assert np.array_equal(att.cpu().numpy(), eager), f"replay {it}"
+            kv.attention(it % layers, heads, qs[it % layers], L - 1)  # eager work between replays
