@@ -157,9 +157,13 @@ __device__ __forceinline__ void compute_tiles(const TileBuf<D> &b, int kbeg, int
     const float mref = (mnew == -INFINITY) ? 0.f : mnew;
     const float alpha = exp2_fast((st.m - mref) * kLog2e);
     st.m = mnew;
-    st.l *= alpha;
+    // alpha is exactly 1.0 where the max did not move; once the max settles
+    // that holds for the whole wave and the rescale (a no-op) is skipped.
+    if (!__all(alpha == 1.0f)) {
+        st.l *= alpha;
 #pragma unroll
-    for (int db = 0; db < S::DB; db++) st.o[db] *= alpha;
+        for (int db = 0; db < S::DB; db++) st.o[db] *= alpha;
+    }
     float lsum = 0.f;
 #pragma unroll
     for (int u = 0; u < S::TG; u++) {
@@ -337,20 +341,18 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 
 // Merge pass: workgroup (unit, column, 16-dim slice) combines the nchunks
 // (<= 256) partial states of one query head for 16 of its head dims.  Thread
-// (grp, dd) of 16 groups owns children grp, grp + 16, ...; all of its O loads
-// and the (m, l) loads (one child per thread) are issued before any is used,
-// so the pass costs one memory round trip.  Per-thread sums run in child
-// order and the group sums are combined in group order: deterministic for a
-// given nchunks.
+// (grp, dd) of 16 groups owns children grp, grp + 16, ...: it loads their O, m
+// and l together (one memory round trip), merges them by log-sum-exp against
+// its own running max, and a single LDS step combines the 16 group states the
+// same way.  Child order within a thread and group order in the combine are
+// fixed: deterministic for a given nchunks.
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
     constexpr int DW = 16;                        // head dims per workgroup
     constexpr int NS = D / DW;                    // slices per column
     constexpr int G = 256 / DW;                   // thread groups over children
     constexpr int NB = kDecodeMaxChunks / G;      // children per thread
-    __shared__ float sw[kDecodeMaxChunks];
-    __shared__ float red[4];
-    __shared__ float so[G][DW];
+    __shared__ float sm[G][DW], so[G][DW], sl[G][DW];
     const int units = a.kv_heads * a.hslices;
     const int ds = blockIdx.x % NS, col = (blockIdx.x / NS) % 16, unit = blockIdx.x / (NS * 16);
     const int kvh = unit / a.hslices, slice = unit % a.hslices;
@@ -359,46 +361,46 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
     const DecodeSpace<D> ws(a.part, units);
     const size_t base = DecodeSpace<D>::at(unit, col, 0);
     const float *o = ws.o + base * D + ds * DW, *m = ws.m + base, *l = ws.l + base;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x;
     const int grp = tid / DW, dd = tid % DW;
     const int n = a.nchunks;
 
-    float v[NB];
+    float vo[NB], vm[NB], vl[NB];
 #pragma unroll
     for (int u = 0; u < NB; u++) {
         const int ch = grp + u * G;
-        v[u] = ch < n ? o[(size_t)ch * D + dd] : 0.f;
+        const bool live = ch < n;
+        vo[u] = live ? o[(size_t)ch * D + dd] : 0.f;
+        vm[u] = live ? m[ch] : -INFINITY;
+        vl[u] = live ? l[ch] : 0.f;
     }
-    const float mv = tid < n ? m[tid] : -INFINITY;
-    const float lv = tid < n ? l[tid] : 0.f;
-    float M = mv;
+    float M = -INFINITY;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-    if (lane == 0) red[w] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float e = exp2_fast((mv - M) * kLog2e);  // 0 for absent children
-    sw[tid] = e;
-    float L = lv * e;
+    for (int u = 0; u < NB; u++) M = fmaxf(M, vm[u]);
+    const float Mref = (M == -INFINITY) ? 0.f : M;  // a group with no children
+    float acc = 0.f, L = 0.f;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off);
-    __syncthreads();
-    if (lane == 0) red[w] = L;
-    __syncthreads();
-    L = (red[0] + red[1]) + (red[2] + red[3]);
-
-    // Branch-free: absent children have v = 0 and weight 0, so the weight
-    // reads are issued together instead of one LDS round trip per child.
-    float acc = 0.f;
-#pragma unroll
-    for (int u = 0; u < NB; u++) acc += v[u] * sw[grp + u * G];
+    for (int u = 0; u < NB; u++) {
+        const float e = exp2_fast((vm[u] - Mref) * kLog2e);
+        acc += vo[u] * e;
+        L += vl[u] * e;
+    }
+    sm[grp][dd] = M;
     so[grp][dd] = acc;
+    sl[grp][dd] = L;
     __syncthreads();
     if (tid < DW) {
-        float s = 0.f;
+        float Mt = -INFINITY;
 #pragma unroll
-        for (int gg = 0; gg < G; gg++) s += so[gg][tid];
-        a.att[(size_t)(kvh * a.group + col0 + col) * D + ds * DW + tid] = s / L;
+        for (int gg = 0; gg < G; gg++) Mt = fmaxf(Mt, sm[gg][tid]);
+        float ot = 0.f, Lt = 0.f;
+#pragma unroll
+        for (int gg = 0; gg < G; gg++) {
+            const float e = exp2_fast((sm[gg][tid] - Mt) * kLog2e);  // 0 for empty groups
+            ot += so[gg][tid] * e;
+            Lt += sl[gg][tid] * e;
+        }
+        a.att[(size_t)(kvh * a.group + col0 + col) * D + ds * DW + tid] = ot / Lt;
     }
 }
 
