@@ -75,6 +75,42 @@ int wick_hip_kv_append_device(wick_hip_kv *kv, int layer, int start, int t, cons
 int wick_hip_attention_device(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int t, int start,
                               float *att_dev);
 
+/* ---- input preparation on the device: the per-token part of Model::forward
+ *      that produces what attention reads (src/model.rs:464-484): bias add,
+ *      QK-norm, RoPE of q and k, and the cache append.  The prepared q and the
+ *      appended k, v are bit-identical to wick's CPU arithmetic. */
+
+/* RoPE table: (sin, cos) of the f32 angle pos * inv_freq[i] for every cache
+ * position pos < capacity, computed on the host with the C library's sinf and
+ * cosf (the calls f32::sin_cos makes in rope, src/model.rs:404-414) and kept
+ * on the device.  inv_freq is a host array [head_dim/2]
+ * (Config::rope_inv_freq, src/config.rs:153-185).  Synchronous. */
+int wick_hip_kv_set_rope(wick_hip_kv *kv, const float *inv_freq);
+
+/* Per-layer constants of the preparation (src/model.rs:470-478), host arrays
+ * copied to the device: biases bq [heads*head_dim], bk and bv
+ * [kv_heads*head_dim] (all three or none: wick adds them only when all three
+ * exist), QK-norm weights q_norm and k_norm [head_dim] (both or none), and
+ * the RMSNorm eps.  Call it for every layer that wick_hip_attend will see,
+ * with NULLs for a model that has neither.  Synchronous. */
+int wick_hip_kv_set_prep(wick_hip_kv *kv, int layer, int heads, const float *bq, const float *bk, const float *bv,
+                         const float *q_norm, const float *k_norm, float eps);
+
+/* src/model.rs:464-485 for one layer: q [t][heads*head_dim], k and v
+ * [t][kv_heads*head_dim] are the raw projections (host arrays) of the tokens
+ * at positions start..start+t.  Applies bias, QK-norm and RoPE to q and k as
+ * the CPU does (bit-identical), appends k and v at start.., then runs
+ * Model::attention; att [t][heads*head_dim] is fully overwritten.  q, k and v
+ * are not modified.  Needs wick_hip_kv_set_rope and wick_hip_kv_set_prep
+ * (same heads) first.  Synchronous. */
+int wick_hip_attend(wick_hip_kv *kv, int layer, int heads, const float *q, const float *k, const float *v, int t,
+                    int start, float *att);
+
+/* As wick_hip_attend on device arrays; q_dev is rewritten in place with the
+ * prepared q.  Asynchronous on the handle's stream. */
+int wick_hip_attend_device(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev,
+                           const float *v_dev, int t, int start, float *att_dev);
+
 /* Make the handle launch on `stream` (a hipStream_t; NULL = the handle's own
  * stream, not the legacy default stream).  Set it before the first call. */
 int wick_hip_kv_set_stream(wick_hip_kv *kv, void *stream);

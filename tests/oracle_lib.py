@@ -82,6 +82,33 @@ def rmsnorm(x, w, eps):
     return out
 
 
+def rmsnorm_inplace(x, w, eps):
+    """wo_rmsnorm_inplace (src/kernels.rs:351-357) on a copy of x."""
+    x, w = _c(x).copy(), _c(w)
+    load().wo_rmsnorm_inplace(_p(x), _p(w), eps, x.size)
+    return x
+
+
+def prep(q, k, v, heads, kv_heads, head_dim, start, inv_freq, bias=None, norms=None, eps=1e-6):
+    """The per-token preparation of Model::forward (src/model.rs:464-480) on the CPU:
+    bias add, per-head QK-norm, RoPE at positions start.. .  Returns new arrays."""
+    q, k, v = _c(q).copy(), _c(k).copy(), _c(v).copy()
+    d = head_dim
+    for i in range(q.shape[0]):
+        if bias is not None:
+            q[i] += bias[0]
+            k[i] += bias[1]
+            v[i] += bias[2]
+        if norms is not None:
+            for h in range(heads):
+                q[i, h * d:(h + 1) * d] = rmsnorm_inplace(q[i, h * d:(h + 1) * d], norms[0], eps)
+            for h in range(kv_heads):
+                k[i, h * d:(h + 1) * d] = rmsnorm_inplace(k[i, h * d:(h + 1) * d], norms[1], eps)
+        q[i] = rope(q[i], d, start + i, inv_freq)
+        k[i] = rope(k[i], d, start + i, inv_freq)
+    return q, k, v
+
+
 def rope(v, head_dim, pos, inv_freq):
     v = _c(v).copy()
     inv = _c(inv_freq)

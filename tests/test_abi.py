@@ -41,6 +41,11 @@ def test_argument_errors_without_device_work():
     assert lib.wick_hip_kv_set_option(None, 1, 64) == _native.EINVAL
     assert lib.wick_hip_attention(None, 0, 4, None, 1, 0, None) == _native.EINVAL
     assert lib.wick_hip_kv_last_grid(None) == 0
+    assert lib.wick_hip_kv_set_rope(None, None) == _native.EINVAL
+    assert lib.wick_hip_kv_set_prep(None, 0, 4, None, None, None, None, None, ctypes.c_float(1e-6)) == _native.EINVAL
+    assert lib.wick_hip_attend(None, 0, 4, None, None, None, 1, 0, None) == _native.EINVAL
+    assert lib.wick_hip_attend_device(None, 0, 4, None, None, None, 1, 0, None) == _native.EINVAL
+    assert b"null" in lib.wick_hip_last_error()
 
 
 def test_no_device_is_an_error_not_a_fallback():

@@ -156,6 +156,39 @@ def test_rope_preserves_pair_norm_and_is_identity_at_zero():
         assert np.allclose(a * a + b * b, ra * ra + rb * rb, rtol=1e-5, atol=1e-6)
 
 
+def test_prep_composition_order_and_special_cases():
+    """ol.prep = bias, then per-head QK-norm, then RoPE (src/model.rs:470-480); v gets the bias only."""
+    rng = np.random.default_rng(4)
+    heads, kv_heads, d = 4, 2, 32
+    inv = ol.rope_inv_freq(10000.0, d)
+    q = rng.standard_normal((3, heads * d)).astype(np.float32)
+    k = rng.standard_normal((3, kv_heads * d)).astype(np.float32)
+    v = rng.standard_normal((3, kv_heads * d)).astype(np.float32)
+    bias = (rng.standard_normal(heads * d).astype(np.float32), rng.standard_normal(kv_heads * d).astype(np.float32),
+            rng.standard_normal(kv_heads * d).astype(np.float32))
+    norms = (rng.uniform(0.5, 1.5, d).astype(np.float32), rng.uniform(0.5, 1.5, d).astype(np.float32))
+    # position 0 without constants: identity, bit for bit
+    pq, pk, pv = ol.prep(q[:1], k[:1], v[:1], heads, kv_heads, d, 0, inv)
+    assert np.array_equal(pq, q[:1]) and np.array_equal(pk, k[:1]) and np.array_equal(pv, v[:1])
+    # position 0 with bias and norm: RoPE is the identity, so q = rmsnorm(q + bq) per head
+    pq, pk, pv = ol.prep(q[:1], k[:1], v[:1], heads, kv_heads, d, 0, inv, bias=bias, norms=norms, eps=1e-6)
+    assert np.array_equal(pv[0], v[0] + bias[2])
+    for h in range(heads):
+        want = ol.rmsnorm(q[0, h * d:(h + 1) * d] + bias[0][h * d:(h + 1) * d], norms[0], 1e-6)
+        assert np.array_equal(pq[0, h * d:(h + 1) * d], want)
+    # rmsnorm_inplace and rmsnorm are the same arithmetic
+    assert np.array_equal(ol.rmsnorm_inplace(q[0, :d], norms[0], 1e-6), ol.rmsnorm(q[0, :d], norms[0], 1e-6))
+    # later positions: an f64 restatement agrees to f32 rounding, and v is not rotated
+    pq, pk, pv = ol.prep(q, k, v, heads, kv_heads, d, 50, inv, bias=bias, norms=norms, eps=1e-6)
+    assert np.array_equal(pv, v + np.stack([bias[2]] * 3))
+    x = (q.astype(np.float64) + bias[0]).reshape(3, heads, d)
+    x = x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6) * norms[0]
+    ang = (np.arange(50, 53)[:, None] * inv[None, :].astype(np.float64))[:, None, :]
+    a, b = x[..., :d // 2], x[..., d // 2:]
+    want = np.concatenate([a * np.cos(ang) - b * np.sin(ang), b * np.cos(ang) + a * np.sin(ang)], -1)
+    assert np.allclose(pq.reshape(3, heads, d), want, atol=2e-6, rtol=1e-5)
+
+
 def test_inv_freq_closed_forms_and_host_agreement():
     for theta, d in ((10000.0, 64), (1e6, 128), (500000.0, 128), (50000.0, 16)):
         inv = ol.rope_inv_freq(theta, d)

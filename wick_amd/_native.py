@@ -37,6 +37,10 @@ SIGNATURES = {
     "wick_hip_kv_synchronize": (_I, [_P]),
     "wick_hip_kv_set_option": (_I, [_P, _I, _I]),
     "wick_hip_kv_last_grid": (_I, [_P]),
+    "wick_hip_kv_set_rope": (_I, [_P, _P]),
+    "wick_hip_kv_set_prep": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, ctypes.c_float]),
+    "wick_hip_attend": (_I, [_P, _I, _I, _P, _P, _P, _I, _I, _P]),
+    "wick_hip_attend_device": (_I, [_P, _I, _I, _P, _P, _P, _I, _I, _P]),
 }
 
 _lib = None

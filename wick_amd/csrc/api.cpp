@@ -11,7 +11,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <cmath>
 #include <string>
+#include <vector>
 
 #include "attn_kernels.h"
 
@@ -57,6 +59,15 @@ struct wick_hip_kv {
     // options
     int decode_chunk = 0, pairing = -1, prefill_split = 1, last_grid = 0;
     int decode_blocks_per_cu = 1;
+    // input preparation (wick_hip_kv_set_rope / wick_hip_kv_set_prep)
+    float *rope_cos = nullptr, *rope_sin = nullptr;  // [capacity][head_dim/2]
+    struct LayerPrep {
+        float *buf = nullptr;  // bq [heads*D] | bk [kvd] | bv [kvd] | q_norm [D] | k_norm [D]
+        int heads = 0;
+        bool set = false, bias = false, norm = false;
+        float eps = 0.0f;
+    };
+    std::vector<LayerPrep> prep;
 
     size_t layer_floats() const { return (size_t)kv_heads * capacity * head_dim; }
     float *k_layer(int l) const { return k + (size_t)l * layer_floats(); }
@@ -176,6 +187,44 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
     return WICK_HIP_OK;
 }
 
+// Bias, QK-norm and RoPE of q (in place) and k, and the append of k and v
+// (src/model.rs:464-484), for tokens at start..start+t of `layer`.
+int run_prep(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev, const float *v_dev, int t,
+             int start) {
+    if (!kv->rope_cos) return fail(WICK_HIP_EINVAL, "no RoPE table (call wick_hip_kv_set_rope first)");
+    const wick_hip_kv::LayerPrep &p = kv->prep[layer];
+    if (!p.set) return fail(WICK_HIP_EINVAL, "layer %d has no preparation constants (call wick_hip_kv_set_prep)", layer);
+    if (heads != p.heads)
+        return fail(WICK_HIP_EINVAL, "heads %d differs from the %d given to wick_hip_kv_set_prep", heads, p.heads);
+    const int D = kv->head_dim, kvd = kv->kv_heads * D;
+    wick::PrepArgs a{};
+    a.q = q_dev;
+    a.ksrc = k_dev;
+    a.vsrc = v_dev;
+    a.k = kv->k_layer(layer);
+    a.v = kv->v_layer(layer);
+    if (p.bias) {
+        a.bq = p.buf;
+        a.bk = p.buf + (size_t)heads * D;
+        a.bv = a.bk + kvd;
+    }
+    if (p.norm) {
+        a.qn = p.buf + (size_t)heads * D + 2 * kvd;
+        a.kn = a.qn + D;
+    }
+    a.rope_cos = kv->rope_cos;
+    a.rope_sin = kv->rope_sin;
+    a.capacity = kv->capacity;
+    a.start = start;
+    a.t = t;
+    a.heads = heads;
+    a.kv_heads = kv->kv_heads;
+    a.eps = p.eps;
+    hipError_t e = wick::launch_prep(D, a, kv->stream);
+    if (e != hipSuccess) return hip_fail(e, "prep kernel launch");
+    return WICK_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -206,6 +255,7 @@ int wick_hip_kv_create(int layers, int capacity, int kv_heads, int head_dim, wic
             break;
         }
         kv->num_cus = prop.multiProcessorCount;
+        kv->prep.resize(layers);
         kv->decode_blocks_per_cu = wick::decode_blocks_per_cu(head_dim);
         if ((e = hipStreamCreateWithFlags(&kv->own_stream, hipStreamNonBlocking)) != hipSuccess) { rc = hip_fail(e, "hipStreamCreate"); break; }
         kv->stream = kv->own_stream;
@@ -231,6 +281,10 @@ void wick_hip_kv_destroy(wick_hip_kv *kv) {
     float *bufs[] = {kv->k, kv->v, kv->q_dev, kv->att_dev, kv->kst_dev, kv->vst_dev, kv->part};
     for (float *b : bufs)
         if (b) (void)hipFree(b);
+    if (kv->rope_cos) (void)hipFree(kv->rope_cos);
+    if (kv->rope_sin) (void)hipFree(kv->rope_sin);
+    for (auto &p : kv->prep)
+        if (p.buf) (void)hipFree(p.buf);
     if (kv->own_stream) (void)hipStreamDestroy(kv->own_stream);
     delete kv;
 }
@@ -339,6 +393,111 @@ int wick_hip_attention(wick_hip_kv *kv, int layer, int heads, const float *q, in
     HIP_TRY(hipMemcpyAsync(kv->q_dev, q, n * sizeof(float), hipMemcpyHostToDevice, kv->stream));
     if ((rc = run_attention(kv, layer, heads, kv->q_dev, t, start, kv->att_dev))) return rc;
     HIP_TRY(hipMemcpyAsync(att, kv->att_dev, n * sizeof(float), hipMemcpyDeviceToHost, kv->stream));
+    HIP_TRY(hipStreamSynchronize(kv->stream));
+    return WICK_HIP_OK;
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int wick_hip_kv_set_rope(wick_hip_kv *kv, const float *inv_freq) {
+    if (!kv) return fail(WICK_HIP_EINVAL, "null cache handle");
+    if (!inv_freq) return fail(WICK_HIP_EINVAL, "null inv_freq");
+    const int H = kv->head_dim / 2;
+    const size_t n = (size_t)kv->capacity * H;
+    std::vector<float> c(n), s(n);
+    for (int pos = 0; pos < kv->capacity; pos++)
+        for (int i = 0; i < H; i++) {
+            // rope (src/model.rs:408): (pos as f32 * inv_freq[i]).sin_cos()
+            const float ang = (float)pos * inv_freq[i];
+            s[(size_t)pos * H + i] = sinf(ang);
+            c[(size_t)pos * H + i] = cosf(ang);
+        }
+    if (!kv->rope_cos) HIP_TRY(hipMalloc(&kv->rope_cos, n * sizeof(float)));
+    if (!kv->rope_sin) HIP_TRY(hipMalloc(&kv->rope_sin, n * sizeof(float)));
+    HIP_TRY(hipMemcpyAsync(kv->rope_cos, c.data(), n * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+    HIP_TRY(hipMemcpyAsync(kv->rope_sin, s.data(), n * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+    HIP_TRY(hipStreamSynchronize(kv->stream));
+    return WICK_HIP_OK;
+}
+
+int wick_hip_kv_set_prep(wick_hip_kv *kv, int layer, int heads, const float *bq, const float *bk, const float *bv,
+                         const float *q_norm, const float *k_norm, float eps) {
+    int rc = check_kv(kv, layer);
+    if (rc) return rc;
+    if (heads < 1 || heads % kv->kv_heads != 0)
+        return fail(WICK_HIP_EINVAL, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv->kv_heads);
+    const int nb = (bq != nullptr) + (bk != nullptr) + (bv != nullptr);
+    if (nb != 0 && nb != 3) return fail(WICK_HIP_EINVAL, "give all three of bq, bk, bv or none");
+    if ((q_norm != nullptr) != (k_norm != nullptr)) return fail(WICK_HIP_EINVAL, "give both q_norm and k_norm or neither");
+    if (!(eps >= 0.0f)) return fail(WICK_HIP_EINVAL, "eps must be >= 0");
+    const int D = kv->head_dim, kvd = kv->kv_heads * D;
+    wick_hip_kv::LayerPrep &p = kv->prep[layer];
+    const size_t need = (size_t)heads * D + 2 * (size_t)kvd + 2 * (size_t)D;
+    if (p.buf && p.heads != heads) {
+        HIP_TRY(hipStreamSynchronize(kv->stream));
+        (void)hipFree(p.buf);
+        p.buf = nullptr;
+    }
+    p.set = false;
+    if (!p.buf) HIP_TRY(hipMalloc(&p.buf, need * sizeof(float)));
+    p.heads = heads;
+    p.bias = nb == 3;
+    p.norm = q_norm != nullptr;
+    p.eps = eps;
+    if (p.bias) {
+        HIP_TRY(hipMemcpyAsync(p.buf, bq, (size_t)heads * D * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+        HIP_TRY(hipMemcpyAsync(p.buf + (size_t)heads * D, bk, kvd * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+        HIP_TRY(hipMemcpyAsync(p.buf + (size_t)heads * D + kvd, bv, kvd * sizeof(float), hipMemcpyHostToDevice,
+                               kv->stream));
+    }
+    if (p.norm) {
+        float *qn = p.buf + (size_t)heads * D + 2 * kvd;
+        HIP_TRY(hipMemcpyAsync(qn, q_norm, D * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+        HIP_TRY(hipMemcpyAsync(qn + D, k_norm, D * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(kv->stream));
+    p.set = true;
+    return WICK_HIP_OK;
+}
+
+int wick_hip_attend_device(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev,
+                           const float *v_dev, int t, int start, float *att_dev) {
+    int rc = check_kv(kv, layer);
+    if (rc) return rc;
+    if ((rc = check_span(kv, start, t))) return rc;
+    if (!q_dev || !k_dev || !v_dev || !att_dev) return fail(WICK_HIP_EINVAL, "null q, k, v or att");
+    if (heads < 1 || heads % kv->kv_heads != 0)
+        return fail(WICK_HIP_EINVAL, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv->kv_heads);
+    if ((rc = run_prep(kv, layer, heads, q_dev, k_dev, v_dev, t, start))) return rc;
+    return run_attention(kv, layer, heads, q_dev, t, start, att_dev);
+}
+
+int wick_hip_attend(wick_hip_kv *kv, int layer, int heads, const float *q, const float *k, const float *v, int t,
+                    int start, float *att) {
+    int rc = check_kv(kv, layer);
+    if (rc) return rc;
+    if ((rc = check_span(kv, start, t))) return rc;
+    if (!q || !k || !v || !att) return fail(WICK_HIP_EINVAL, "null q, k, v or att");
+    if (heads < 1 || heads % kv->kv_heads != 0)
+        return fail(WICK_HIP_EINVAL, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv->kv_heads);
+    const size_t nq = (size_t)t * heads * kv->head_dim, nk = (size_t)t * kv->kv_heads * kv->head_dim;
+    if ((rc = grow(&kv->q_dev, &kv->q_cap, nq, "hipMalloc(q staging)"))) return rc;
+    if ((rc = grow(&kv->att_dev, &kv->att_cap, nq, "hipMalloc(att staging)"))) return rc;
+    if (nk > kv->kst_cap) {
+        size_t ck = kv->kst_cap, cv = kv->kst_cap;
+        kv->kst_cap = 0;
+        if ((rc = grow(&kv->kst_dev, &ck, nk, "hipMalloc(k staging)"))) return rc;
+        if ((rc = grow(&kv->vst_dev, &cv, nk, "hipMalloc(v staging)"))) return rc;
+        kv->kst_cap = nk;
+    }
+    HIP_TRY(hipMemcpyAsync(kv->q_dev, q, nq * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+    HIP_TRY(hipMemcpyAsync(kv->kst_dev, k, nk * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+    HIP_TRY(hipMemcpyAsync(kv->vst_dev, v, nk * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+    if ((rc = run_prep(kv, layer, heads, kv->q_dev, kv->kst_dev, kv->vst_dev, t, start))) return rc;
+    if ((rc = run_attention(kv, layer, heads, kv->q_dev, t, start, kv->att_dev))) return rc;
+    HIP_TRY(hipMemcpyAsync(att, kv->att_dev, nq * sizeof(float), hipMemcpyDeviceToHost, kv->stream));
     HIP_TRY(hipStreamSynchronize(kv->stream));
     return WICK_HIP_OK;
 }

@@ -37,6 +37,17 @@ struct AppendArgs {
     int capacity, start, t, kv_heads;
 };
 
+struct PrepArgs {
+    float *q;                        // [t][heads*D], rewritten in place
+    const float *ksrc, *vsrc;        // [t][kv_heads*D]
+    float *k, *v;                    // layer base, [kv_heads][capacity][D]
+    const float *bq, *bk, *bv;       // [heads*D], [kv_heads*D], [kv_heads*D] or null (no bias)
+    const float *qn, *kn;            // [D] or null (no QK-norm)
+    const float *rope_cos, *rope_sin;  // [capacity][D/2]
+    int capacity, start, t, heads, kv_heads;
+    float eps;
+};
+
 // Floats of decode workspace needed for `units` (kv head, head slice) pairs.
 size_t decode_workspace_floats(int units, int head_dim);
 
@@ -48,5 +59,7 @@ hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_
 int prefill_grid(const PrefillArgs &a);
 hipError_t launch_prefill(int head_dim, const PrefillArgs &a, hipStream_t s);
 hipError_t launch_append(int head_dim, const AppendArgs &a, hipStream_t s);
+// prep.hip: bias, QK-norm, RoPE of q and k; k and v appended to the cache.
+hipError_t launch_prep(int head_dim, const PrepArgs &a, hipStream_t s);
 
 }  // namespace wick

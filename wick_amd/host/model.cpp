@@ -1,11 +1,13 @@
 // model.cpp -- f32 Model::forward mirror whose KV cache and attention run on the GPU.
 //
-// Mirrors /root/reference/src/model.rs:420-516 step by step.  Every
-// non-attention step keeps wick's f32 operation order (AVX2 dot product with
-// FMA and wick's horizontal sum, src/kernels.rs:196-230; rmsnorm :343-357;
-// rope src/model.rs:404-414; silu_mul src/kernels.rs:373-378), so the only
-// numerical difference from an all-CPU run is the attention itself.  Build
-// with -mavx2 -mfma -ffp-contract=off.
+// Mirrors /root/reference/src/model.rs:420-516 step by step.  Every host step
+// keeps wick's f32 operation order (AVX2 dot product with FMA and wick's
+// horizontal sum, src/kernels.rs:196-230; rmsnorm :343-349; silu_mul
+// src/kernels.rs:373-378).  The per-token preparation (bias, QK-norm, RoPE;
+// src/model.rs:464-480), the cache write and the attention run on the GPU
+// through wick_hip_attend; the preparation there is bit-identical to the CPU's,
+// so the only numerical difference from an all-CPU run is the attention itself.
+// Build with -mavx2 -mfma -ffp-contract=off.
 #include "wick_host.h"
 
 #include <immintrin.h>
@@ -166,21 +168,6 @@ void rmsnorm(const float *x, const float *w, float eps, float *out, int n) {
     for (int i = 0; i < n; i++) out[i] = x[i] * scale * w[i];
 }
 
-// src/model.rs:404-414
-void rope(float *v, int n, int hd, int pos, const float *inv_freq) {
-    const int half = hd / 2;
-    for (int h0 = 0; h0 + hd <= n; h0 += hd) {
-        float *head = v + h0;
-        for (int i = 0; i < half; i++) {
-            const float ang = (float)pos * inv_freq[i];
-            const float s = sinf(ang), c = cosf(ang);
-            const float a = head[i], b = head[i + half];
-            head[i] = a * c - b * s;
-            head[i + half] = b * c + a * s;
-        }
-    }
-}
-
 enum { T_ATTN_NORM, T_WQ, T_WK, T_WV, T_WO, T_BQ, T_BK, T_BV, T_QN, T_KN, T_FFN_NORM, T_GATE, T_UP, T_DOWN };
 
 }  // namespace
@@ -240,6 +227,18 @@ wick_host_state *wick_host_state_create(wick_host_model *m, int capacity) {
         delete s;
         return nullptr;
     }
+    // constants of the device-side input preparation: the RoPE table and, per
+    // layer, the optional biases and QK-norm weights
+    rc = wick_hip_kv_set_rope(s->kv, m->inv_freq);
+    for (int li = 0; rc == WICK_HIP_OK && li < m->c.layers; li++)
+        rc = wick_hip_kv_set_prep(s->kv, li, m->c.heads, m->L(li, T_BQ), m->L(li, T_BK), m->L(li, T_BV), m->L(li, T_QN),
+                                  m->L(li, T_KN), m->c.rms_eps);
+    if (rc != WICK_HIP_OK) {
+        g_err = std::string("wick_hip_kv_set_rope/set_prep: ") + wick_hip_last_error();
+        wick_hip_kv_destroy(s->kv);
+        delete s;
+        return nullptr;
+    }
     s->capacity = capacity;
     return s;
 }
@@ -295,25 +294,8 @@ int wick_host_forward(wick_host_model *m, wick_host_state *s, const uint32_t *to
         for (int i = 0; i < t; i++) rmsnorm(x + (size_t)i * h, m->L(li, T_ATTN_NORM), c.rms_eps, xn + (size_t)i * h, h);
         matmul(m->pool, {{m->L(li, T_WQ), qd, q, qd}, {m->L(li, T_WK), kvd, k, kvd}, {m->L(li, T_WV), kvd, v, kvd}}, xn, t,
                h);
-        const float *bq = m->L(li, T_BQ), *bk = m->L(li, T_BK), *bv = m->L(li, T_BV);
-        const float *qn = m->L(li, T_QN), *kn = m->L(li, T_KN);
-        for (int i = 0; i < t; i++) {
-            float *qi = q + (size_t)i * qd, *ki = k + (size_t)i * kvd, *vi = v + (size_t)i * kvd;
-            if (bq && bk && bv) {
-                for (int j = 0; j < qd; j++) qi[j] += bq[j];
-                for (int j = 0; j < kvd; j++) ki[j] += bk[j];
-                for (int j = 0; j < kvd; j++) vi[j] += bv[j];
-            }
-            if (qn && kn) {
-                for (int j = 0; j < qd; j += hd) rmsnorm(qi + j, qn, c.rms_eps, qi + j, hd);
-                for (int j = 0; j < kvd; j += hd) rmsnorm(ki + j, kn, c.rms_eps, ki + j, hd);
-            }
-            rope(qi, qd, hd, start + i, m->inv_freq);
-            rope(ki, kvd, hd, start + i, m->inv_freq);
-        }
-        // the cache write of src/model.rs:481-483, then Model::attention (:485), on the GPU
-        int rc = wick_hip_kv_append(s->kv, li, start, t, k, v);
-        if (rc == WICK_HIP_OK) rc = wick_hip_attention(s->kv, li, c.heads, q, t, start, att);
+        // src/model.rs:464-485 on the GPU: bias, QK-norm, RoPE, the cache write and Model::attention
+        int rc = wick_hip_attend(s->kv, li, c.heads, q, k, v, t, start, att);
         if (rc != WICK_HIP_OK) {
             g_err = std::string("attention: ") + wick_hip_last_error();
             return rc;

@@ -4,6 +4,7 @@ Mirrors, over the C ABI, what wick's Rust code holds and calls:
   KvCache       /root/reference/src/model.rs:251-275 (now [layer][kv_head][pos][head_dim] in HBM)
   cache append  /root/reference/src/model.rs:481-483
   attention     /root/reference/src/model.rs:518-553 (called per layer at :485)
+  input prep    /root/reference/src/model.rs:464-484 (bias, QK-norm, RoPE, append) via attend()
 """
 import ctypes
 
@@ -72,7 +73,35 @@ class DeviceKvCache:
         _native.check(self._lib.wick_hip_attention(self.handle, layer, heads, _ptr(q), q.shape[0], start, _ptr(att)))
         return att
 
+    def set_rope(self, inv_freq):
+        """RoPE table for attend(): inv_freq [head_dim/2] as Config::rope_inv_freq gives it."""
+        f = _f32(inv_freq).reshape(-1)
+        assert f.size == self.head_dim // 2
+        _native.check(self._lib.wick_hip_kv_set_rope(self.handle, _ptr(f)))
+
+    def set_prep(self, layer, heads, bq=None, bk=None, bv=None, q_norm=None, k_norm=None, eps=1e-6):
+        """Per-layer bias / QK-norm constants for attend() (None = absent)."""
+        arrs = [None if a is None else _f32(a).reshape(-1) for a in (bq, bk, bv, q_norm, k_norm)]
+        ptrs = [None if a is None else _ptr(a) for a in arrs]
+        _native.check(self._lib.wick_hip_kv_set_prep(self.handle, layer, heads, *ptrs, ctypes.c_float(eps)))
+
+    def attend(self, layer, heads, q, k, v, start):
+        """src/model.rs:464-485 for one layer: raw projections q, k, v of t tokens in,
+        attention output out; k and v are prepared and appended at start.."""
+        q = _f32(q).reshape(-1, heads * self.head_dim)
+        k, v = _f32(k).reshape(-1, self.kv_dim), _f32(v).reshape(-1, self.kv_dim)
+        assert k.shape[0] == q.shape[0] and v.shape == k.shape
+        att = np.empty_like(q)
+        _native.check(self._lib.wick_hip_attend(self.handle, layer, heads, _ptr(q), _ptr(k), _ptr(v), q.shape[0],
+                                                start, _ptr(att)))
+        return att
+
     # ---- device-pointer entry points (asynchronous on the handle's stream)
+    def attend_device(self, layer, heads, q_ptr, k_ptr, v_ptr, t, start, att_ptr):
+        _native.check(self._lib.wick_hip_attend_device(self.handle, layer, heads, ctypes.c_void_p(q_ptr),
+                                                       ctypes.c_void_p(k_ptr), ctypes.c_void_p(v_ptr), t, start,
+                                                       ctypes.c_void_p(att_ptr)))
+
     def append_device(self, layer, start, t, k_ptr, v_ptr):
         _native.check(self._lib.wick_hip_kv_append_device(self.handle, layer, start, t, ctypes.c_void_p(k_ptr),
                                                           ctypes.c_void_p(v_ptr)))
