@@ -1,4 +1,4 @@
-"""The C ABI library loads and exports every symbol include/wick_hip.h declares.
+"""The C ABI library loads and exports every symbol include/*.h declares.
 
 CPU-only: argument checks that fail before any device work are exercised; no
 compute call is made without a GPU.
@@ -15,9 +15,13 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def header_symbols():
-    with open(os.path.join(ROOT, "include", "wick_hip.h")) as f:
-        text = f.read()
-    return set(re.findall(r"\b(wick_hip_\w+)\s*\(", text))
+    names = set()
+    inc = os.path.join(ROOT, "include")
+    for fn in sorted(os.listdir(inc)):
+        if fn.endswith(".h"):
+            with open(os.path.join(inc, fn)) as f:
+                names |= set(re.findall(r"\b(wick_hip_\w+)\s*\(", f.read()))
+    return names
 
 
 def test_header_and_binding_agree():
@@ -46,6 +50,14 @@ def test_argument_errors_without_device_work():
     assert lib.wick_hip_attend(None, 0, 4, None, None, None, 1, 0, None) == _native.EINVAL
     assert lib.wick_hip_attend_device(None, 0, 4, None, None, None, 1, 0, None) == _native.EINVAL
     assert b"null" in lib.wick_hip_last_error()
+    m = ctypes.c_void_p()
+    assert lib.wick_hip_model_create(None, None, None, None, None, None, ctypes.byref(m)) == _native.EINVAL
+    assert lib.wick_hip_model_create(None, None, None, None, None, None, None) == _native.EINVAL
+    lib.wick_hip_model_destroy(None)
+    assert lib.wick_hip_model_new_cache(None, 16, ctypes.byref(m)) == _native.EINVAL
+    assert lib.wick_hip_model_forward(None, None, None, 1, 0, 0, None) == _native.EINVAL
+    assert lib.wick_hip_model_prefill(None, None, None, 1, 0, None) == _native.EINVAL
+    assert lib.wick_hip_model_decode(None, None, 0, 0, 1, None) == _native.EINVAL
 
 
 def test_no_device_is_an_error_not_a_fallback():

@@ -1,0 +1,159 @@
+"""The device-resident forward (include/wick_hip_model.h) against the CPU oracle
+and the reference's transformers-scored tiny fixtures.
+
+Thresholds are the reference's own (tests/tiny_models.rs): logits within 1e-3
+of transformers (:68), a reordered computation of the same forward within
+1e-4 (:89, chunked vs batch; here GPU vs CPU accumulation order), and greedy
+ids identical (:111).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from wick_amd import _native
+from wick_amd.device_model import DeviceModel
+from wick_amd.model import Config, load_weights
+from wick_amd.synthetic import random_prompt, random_weights, smollm2_135m
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny")
+MODELS = ["llama3-scaled-f32", "qwen2-bias-bf16", "qwen3-qknorm-f32"]
+
+
+def fixture(name):
+    d = os.path.join(GOLDEN, name)
+    cfg = Config.load(d)
+    with open(os.path.join(d, "expected.json")) as f:
+        exp = json.load(f)
+    return cfg, load_weights(d, cfg), exp
+
+
+@pytest.mark.parametrize("name", MODELS)
+def test_tiny_logits_match_transformers_and_cpu(name):
+    cfg, w, exp = fixture(name)
+    with DeviceModel(cfg, w) as m:
+        got = m.forward(m.new_cache(256), exp["tokens"], all_logits=True)
+    worst = np.abs(got - np.array(exp["logits"], np.float32)).max()
+    assert worst < 1e-3, f"{name}: logits differ from transformers by {worst}"
+    om = ol.OracleModel(cfg, w)
+    want = om.forward(om.new_state(256), exp["tokens"], all_logits=True)
+    d = np.abs(got - want).max()
+    print(f"{name}: max |gpu - cpu| over {got.size} logits = {d:.2e}")
+    assert d < 1e-4
+
+
+@pytest.mark.parametrize("name", MODELS)
+def test_tiny_incremental_matches_batch(name):
+    cfg, w, exp = fixture(name)
+    with DeviceModel(cfg, w) as m:
+        batch = m.forward(m.new_cache(256), exp["tokens"], all_logits=True)
+        cache = m.new_cache(256)
+        pos = 0
+        for size in [1, 5, 2, 7, 1, 1, 13, 3, 15]:
+            rows = m.forward(cache, exp["tokens"][pos:pos + size], all_logits=True)
+            d = np.abs(rows - batch[pos:pos + size]).max()
+            assert d < 1e-4, f"{name}: position {pos} differs by {d}"
+            pos += size
+
+
+@pytest.mark.parametrize("name", MODELS)
+def test_tiny_greedy_on_device(name):
+    cfg, w, exp = fixture(name)
+    with DeviceModel(cfg, w) as m:
+        cache = m.new_cache(256)
+        first = m.prefill(cache, exp["greedy_prompt"])
+        ids = [first] + m.decode(cache, first, len(exp["greedy"]) - 1)
+    assert ids == exp["greedy"]
+
+
+def oracle_greedy(cfg, w, prompt, n_gen, capacity):
+    om = ol.OracleModel(cfg, w)
+    st = om.new_state(capacity)
+    logits = om.forward(st, prompt)
+    first_logits = logits[0].copy()
+    ids = []
+    for _ in range(n_gen):
+        tok = ol.argmax(logits[0])
+        ids.append(tok)
+        logits = om.forward(st, [tok])
+    return ids, first_logits
+
+
+def test_smollm2_135m_greedy_ids_match_cpu():
+    """random-init SmolLM2-135M, 128-token prompt, 64 greedy tokens, all on the device."""
+    cfg = smollm2_135m()
+    w = random_weights(cfg, seed=0)
+    prompt = random_prompt(1, 128, cfg.vocab)
+    want, want_logits = oracle_greedy(cfg, w, prompt, 64, 128 + 64 + 8)
+    with DeviceModel(cfg, w) as m:
+        cache = m.new_cache(128 + 64 + 8)
+        logits = m.forward(cache, prompt)
+        d = np.abs(logits[0] - want_logits).max()
+        print(f"prefill logits: max |gpu - cpu| = {d:.2e}")
+        assert d < 1e-4
+        cache.len = 0
+        first = m.prefill(cache, prompt)
+        got = [first] + m.decode(cache, first, 63)
+    assert got == want
+
+
+def test_decode_matches_step_by_step_forward():
+    """decode() keeps ids on the device; forward() + host argmax must give the same chain."""
+    cfg = smollm2_135m()
+    cfg.layers = 4
+    w = random_weights(cfg, seed=3)
+    prompt = random_prompt(4, 40, cfg.vocab)
+    with DeviceModel(cfg, w) as m:
+        c1 = m.new_cache(80)
+        first = m.prefill(c1, prompt)
+        chain = m.decode(c1, first, 20)
+        c2 = m.new_cache(80)
+        logits = m.forward(c2, prompt)
+        assert int(np.argmax(logits[0])) == first
+        tok, steps = first, []
+        for _ in range(20):
+            logits = m.forward(c2, [tok])
+            tok = ol.argmax(logits[0])
+            steps.append(tok)
+        k1, v1 = c1.read(3, 0, 60)
+        k2, v2 = c2.read(3, 0, 60)
+    assert chain == steps
+    assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+
+
+def test_prefill_chunks_of_256():
+    """A 300-token prompt runs as chunks of 256 + 44 (src/engine.rs:107, :134)."""
+    cfg, w, exp = fixture("qwen3-qknorm-f32")
+    rng = np.random.default_rng(7)
+    prompt = [int(x) for x in rng.integers(0, cfg.vocab, 300)]
+    om = ol.OracleModel(cfg, w)
+    want = om.forward(om.new_state(320), prompt)[0]
+    with DeviceModel(cfg, w) as m:
+        cache = m.new_cache(320)
+        nxt = m.prefill(cache, prompt)
+        assert cache.len == 300
+        rows = m.forward(m.new_cache(320), prompt, all_logits=True)
+    assert np.abs(rows[-1] - want).max() < 1e-4
+    assert nxt == ol.argmax(want)
+
+
+def test_model_errors():
+    cfg, w, exp = fixture("llama3-scaled-f32")
+    with DeviceModel(cfg, w) as m:
+        cache = m.new_cache(8)
+        with pytest.raises(_native.WickHipError, match="vocabulary"):
+            m.forward(cache, [cfg.vocab])
+        with pytest.raises(_native.WickHipError, match="context length"):
+            m.forward(cache, list(range(9)))
+        with pytest.raises(_native.WickHipError, match="steps"):
+            m.decode(cache, 1, 0)
+        from wick_amd import DeviceKvCache
+        with DeviceKvCache(cfg.layers, 8, cfg.kv_heads, cfg.head_dim) as other:
+            with pytest.raises(_native.WickHipError, match="stream"):
+                m.forward(other, [1])
+        cache.len = 0
+        assert m.forward(cache, [1, 2, 3]).shape == (1, cfg.vocab)

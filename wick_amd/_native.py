@@ -1,4 +1,4 @@
-"""ctypes bindings of the C ABI in include/wick_hip.h.
+"""ctypes bindings of the C ABI in include/wick_hip.h and include/wick_hip_model.h.
 
 This is the binding a host program writes for the library (the Rust side would
 declare the same symbols in an `extern "C"` block).  There is no fallback: if
@@ -20,7 +20,7 @@ OPT_DECODE_CHUNK = 1
 OPT_PREFILL_PAIRING = 2
 OPT_PREFILL_SPLIT = 3
 
-# Every symbol include/wick_hip.h declares, with its ctypes signature.
+# Every symbol include/*.h declares, with its ctypes signature.
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _FP = ctypes.POINTER(ctypes.c_float)
@@ -41,6 +41,13 @@ SIGNATURES = {
     "wick_hip_kv_set_prep": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, ctypes.c_float]),
     "wick_hip_attend": (_I, [_P, _I, _I, _P, _P, _P, _I, _I, _P]),
     "wick_hip_attend_device": (_I, [_P, _I, _I, _P, _P, _P, _I, _I, _P]),
+    # wick_hip_model.h
+    "wick_hip_model_create": (_I, [_P, _P, _P, _P, _P, _P, ctypes.POINTER(_P)]),
+    "wick_hip_model_destroy": (None, [_P]),
+    "wick_hip_model_new_cache": (_I, [_P, _I, ctypes.POINTER(_P)]),
+    "wick_hip_model_forward": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "wick_hip_model_prefill": (_I, [_P, _P, _P, _I, _I, _P]),
+    "wick_hip_model_decode": (_I, [_P, _P, ctypes.c_uint32, _I, _I, _P]),
 }
 
 _lib = None

@@ -227,6 +227,26 @@ int run_prep(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k
 
 }  // namespace
 
+namespace wick {
+
+int set_error(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+bool kv_info(const wick_hip_kv *kv, KvInfo *out) {
+    if (!kv || !out) return false;
+    *out = KvInfo{kv->layers, kv->capacity, kv->kv_heads, kv->head_dim, kv->stream};
+    return true;
+}
+
+}  // namespace wick
+
 extern "C" {
 
 const char *wick_hip_last_error(void) { return g_last_error.c_str(); }

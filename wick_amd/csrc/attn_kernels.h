@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
+#include "wick_hip.h"
+
 namespace wick {
 
 // Most split-K chunks one decode call uses per (kv head, 16-head slice).
@@ -61,5 +63,15 @@ hipError_t launch_prefill(int head_dim, const PrefillArgs &a, hipStream_t s);
 hipError_t launch_append(int head_dim, const AppendArgs &a, hipStream_t s);
 // prep.hip: bias, QK-norm, RoPE of q and k; k and v appended to the cache.
 hipError_t launch_prep(int head_dim, const PrepArgs &a, hipStream_t s);
+
+// Shape and stream of a cache handle (api.cpp), for the device-resident forward.
+struct KvInfo {
+    int layers, capacity, kv_heads, head_dim;
+    hipStream_t stream;
+};
+bool kv_info(const wick_hip_kv *kv, KvInfo *out);
+
+// Record the message wick_hip_last_error() returns on this thread; returns code.
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 
 }  // namespace wick

@@ -1,0 +1,41 @@
+// Internal interface between the device-resident forward (model_api.cpp) and
+// its HIP kernels (model.hip).  Not installed; the public boundary is
+// include/wick_hip_model.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wick {
+
+// What a gemv_kernel does with the dot products of one output row.
+enum GemvEpilogue {
+    kEpiStore = 0,   // out0[tok][row] = dot
+    kEpiResid = 1,   // out0[tok][row] += dot            (the residual adds of src/model.rs:487, :503)
+    kEpiQkv = 2,     // rows split over out0 / out1 / out2 (q, k, v of src/model.rs:452-462)
+    kEpiSwiglu = 3,  // out0[tok][row] = silu(dot_w) * dot_w2   (silu_mul, src/kernels.rs:373-378)
+};
+
+struct GemvArgs {
+    const float *x;       // input rows [t][cols]
+    const float *norm;    // RMSNorm weight [cols] applied to each input row first, or null
+    const float *w;       // [rows][cols] row-major (wick's layout)
+    const float *w2;      // kEpiSwiglu: the up matrix [rows][cols]
+    float *out0, *out1, *out2;
+    int ld0, ld1, ld2;    // per-token strides (floats) of the outputs
+    int split0, split1;   // kEpiQkv: rows [0,split0) -> out0, [split0,split1) -> out1, the rest -> out2
+    int rows, cols, t;
+    float eps;
+};
+
+// out rows of a matrix-vector (or small matrix-matrix) product with the
+// epilogue `epi`; t tokens, cols % 4 == 0.
+hipError_t launch_gemv(int epi, const GemvArgs &a, hipStream_t s);
+
+// x[i][:] = embed[tokens[i]][:] for i < t (token ids already validated).
+hipError_t launch_embed(const float *embed, const uint32_t *tokens, float *x, int t, int hidden, hipStream_t s);
+
+// *out = sampler::argmax(x[0..n)) (first index of the maximum).
+hipError_t launch_argmax(const float *x, int n, uint32_t *out, hipStream_t s);
+
+}  // namespace wick

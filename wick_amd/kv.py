@@ -35,6 +35,17 @@ class DeviceKvCache:
         # wick's KvCache::len: positions already processed (src/model.rs:256)
         self.len = 0
 
+    @classmethod
+    def adopt(cls, handle, layers, capacity, kv_heads, head_dim):
+        """Wrap a handle made by the library (e.g. wick_hip_model_new_cache); destroyed on close."""
+        self = cls.__new__(cls)
+        self._lib = _native.load()
+        self.handle = handle
+        self.layers, self.capacity, self.kv_heads, self.head_dim = layers, capacity, kv_heads, head_dim
+        self.kv_dim = kv_heads * head_dim
+        self.len = 0
+        return self
+
     def close(self):
         if self.handle:
             self._lib.wick_hip_kv_destroy(self.handle)
