@@ -127,7 +127,12 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
         int rc = ensure_workspace(kv, units);
         if (rc) return rc;
         int chunk = kv->decode_chunk;
-        if (chunk <= 0) {
+        if (chunk <= 0 && len <= wick::kDecodeSingleChunkMax) {
+            // Short context: one workgroup per unit and no merge pass.  Its 4
+            // waves take at most two 32-key groups each, which costs less
+            // than the second launch a split needs.
+            chunk = len;
+        } else if (chunk <= 0) {
             // One resident round: as many chunks as the GPU holds decode
             // workgroups at once, each streaming one long contiguous range.
             const int resident = kv->num_cus * kv->decode_blocks_per_cu;

@@ -11,6 +11,8 @@ namespace wick {
 
 // Most split-K chunks one decode call uses per (kv head, 16-head slice).
 constexpr int kDecodeMaxChunks = 256;
+// Longest context the automatic decode schedule serves with one chunk per unit.
+constexpr int kDecodeSingleChunkMax = 192;
 constexpr int kTileRows = 16;  // query rows (or heads) per MFMA column block
 
 struct DecodeArgs {

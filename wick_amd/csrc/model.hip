@@ -36,20 +36,43 @@ __device__ __forceinline__ float dot4(const f4 w, const f4 x, float acc) {
 
 }  // namespace
 
-// One wave per output row `row`, NT tokens per wave (token group blockIdx.y).
-// Column c4 (a float4 index) of a row is handled by lane c4 % 64.
-template <int NT, int EPI, bool NORM>
+// One wave per R output rows (rows R*wave .. R*wave+R-1), NT tokens per wave
+// (token group blockIdx.y).  Column c4 (a float4 index) of a row is handled by
+// lane c4 % 64; a pass covers 64*UNR float4s of every row.  All loads a pass
+// needs -- weight rows, input rows, norm weight, and the residual being added
+// to -- are issued before the first arithmetic on them, so a kernel whose rows
+// fit one pass waits for memory once.
+template <int NT, int R, int UNR, int EPI, bool NORM>
 __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
-    constexpr int UNR = 4;  // float4 loads per lane in flight per operand
+    static_assert(EPI != kEpiSwiglu || R == 1, "SwiGLU pairs one gate row with one up row");
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= a.rows) return;  // whole waves only; no barriers below
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+    if (row0 >= a.rows) return;  // whole waves only; no barriers below
     const int tok0 = blockIdx.y * NT;
     const int nt = min(NT, a.t - tok0);
     const int C4 = a.cols >> 2;
+    const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     const f4 *X[NT];
 #pragma unroll
     for (int tk = 0; tk < NT; tk++) X[tk] = reinterpret_cast<const f4 *>(a.x + (size_t)(tok0 + min(tk, nt - 1)) * a.cols);
+    const f4 *W[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) W[r] = reinterpret_cast<const f4 *>(a.w + (size_t)min(row0 + r, a.rows - 1) * a.cols);
+    const f4 *W2 = EPI == kEpiSwiglu ? reinterpret_cast<const f4 *>(a.w2 + (size_t)row0 * a.cols) : W[0];
+    const f4 *G = reinterpret_cast<const f4 *>(a.norm);
+
+    // the first pass's weights go out before anything waits on memory
+    f4 wv[R][UNR], wv2[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; u++) {
+        const int c = lane + 64 * u;
+#pragma unroll
+        for (int r = 0; r < R; r++) wv[r][u] = c < C4 ? __builtin_nontemporal_load(W[r] + c) : zero;
+        if (EPI == kEpiSwiglu) wv2[u] = c < C4 ? __builtin_nontemporal_load(W2 + c) : zero;
+    }
+    // the value the residual epilogue adds to (lane tk: token tk)
+    float resid = 0.0f;
+    if (EPI == kEpiResid && lane < nt) resid = a.out0[(size_t)(tok0 + lane) * a.ld0 + row0];
 
     // rmsnorm (src/kernels.rs:343-349) of each input row: xn = x * scale * g
     float scale[NT];
@@ -66,62 +89,73 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
         }
     }
 
-    const f4 *W = reinterpret_cast<const f4 *>(a.w + (size_t)row * a.cols);
-    const f4 *W2 = EPI == kEpiSwiglu ? reinterpret_cast<const f4 *>(a.w2 + (size_t)row * a.cols) : W;
-    const f4 *G = reinterpret_cast<const f4 *>(a.norm);
-    float acc[NT], acc2[NT];
+    float acc[R][NT], acc2[NT];
 #pragma unroll
-    for (int tk = 0; tk < NT; tk++) acc[tk] = acc2[tk] = 0.0f;
-
-    for (int base = lane; base < C4; base += 64 * UNR) {
-        f4 wv[UNR], wv2[UNR];
+    for (int tk = 0; tk < NT; tk++) {
+        acc2[tk] = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r][tk] = 0.0f;
+    }
+    for (int base = 0; base < C4; base += 64 * UNR) {
+        if (base > 0) {
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                const int c = base + lane + 64 * u;
+#pragma unroll
+                for (int r = 0; r < R; r++) wv[r][u] = c < C4 ? __builtin_nontemporal_load(W[r] + c) : zero;
+                if (EPI == kEpiSwiglu) wv2[u] = c < C4 ? __builtin_nontemporal_load(W2 + c) : zero;
+            }
+        }
+        f4 xv[NT][UNR], gv[UNR];
 #pragma unroll
         for (int u = 0; u < UNR; u++) {
-            const int c = base + 64 * u;
-            const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-            wv[u] = c < C4 ? __builtin_nontemporal_load(W + c) : zero;
-            if (EPI == kEpiSwiglu) wv2[u] = c < C4 ? __builtin_nontemporal_load(W2 + c) : zero;
+            const int c = base + lane + 64 * u;
+            if (NORM) gv[u] = c < C4 ? G[c] : zero;
+#pragma unroll
+            for (int tk = 0; tk < NT; tk++) xv[tk][u] = c < C4 ? X[tk][c] : zero;
         }
 #pragma unroll
         for (int u = 0; u < UNR; u++) {
-            const int c = base + 64 * u;
-            if (c < C4) {
-                f4 g = {1.0f, 1.0f, 1.0f, 1.0f};
-                if (NORM) g = G[c];
 #pragma unroll
-                for (int tk = 0; tk < NT; tk++) {
-                    f4 xv = X[tk][c];
-                    if (NORM) xv = xv * scale[tk] * g;
-                    acc[tk] = dot4(wv[u], xv, acc[tk]);
-                    if (EPI == kEpiSwiglu) acc2[tk] = dot4(wv2[u], xv, acc2[tk]);
-                }
+            for (int tk = 0; tk < NT; tk++) {
+                f4 x = xv[tk][u];
+                if (NORM) x = x * scale[tk] * gv[u];
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[r][tk] = dot4(wv[r][u], x, acc[r][tk]);
+                if (EPI == kEpiSwiglu) acc2[tk] = dot4(wv2[u], x, acc2[tk]);
             }
         }
     }
 #pragma unroll
     for (int tk = 0; tk < NT; tk++) {
-        acc[tk] = wave_sum(acc[tk]);
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r][tk] = wave_sum(acc[r][tk]);
         if (EPI == kEpiSwiglu) acc2[tk] = wave_sum(acc2[tk]);
     }
-    // lane tk writes token tk's value
+    // lane tk writes token tk's values
 #pragma unroll
     for (int tk = 0; tk < NT; tk++) {
         if (lane != tk || tk >= nt) continue;
         const size_t tok = (size_t)tok0 + tk;
-        const float d = acc[tk];
-        if (EPI == kEpiStore) {
-            a.out0[tok * a.ld0 + row] = d;
-        } else if (EPI == kEpiResid) {
-            a.out0[tok * a.ld0 + row] += d;
-        } else if (EPI == kEpiQkv) {
-            if (row < a.split0)
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int row = row0 + r;
+            if (row >= a.rows) break;
+            const float d = acc[r][tk];
+            if (EPI == kEpiStore) {
                 a.out0[tok * a.ld0 + row] = d;
-            else if (row < a.split1)
-                a.out1[tok * a.ld1 + (row - a.split0)] = d;
-            else
-                a.out2[tok * a.ld2 + (row - a.split1)] = d;
-        } else {  // silu_mul: g / (1 + exp(-g)) * u
-            a.out0[tok * a.ld0 + row] = d / (1.0f + expf(-d)) * acc2[tk];
+            } else if (EPI == kEpiResid) {
+                a.out0[tok * a.ld0 + row] = resid + d;
+            } else if (EPI == kEpiQkv) {
+                if (row < a.split0)
+                    a.out0[tok * a.ld0 + row] = d;
+                else if (row < a.split1)
+                    a.out1[tok * a.ld1 + (row - a.split0)] = d;
+                else
+                    a.out2[tok * a.ld2 + (row - a.split1)] = d;
+            } else {  // silu_mul: g / (1 + exp(-g)) * u
+                a.out0[tok * a.ld0 + row] = d / (1.0f + expf(-d)) * acc2[tk];
+            }
         }
     }
 }
@@ -137,27 +171,48 @@ __global__ __launch_bounds__(256) void embed_kernel(const float *__restrict__ em
 // sampler::argmax (src/sampler.rs:129-137): best = 0; for i: if x[i] > x[best]
 // { best = i }.  That is the first index of the maximum over the non-NaN
 // values (NaN never compares greater), except that a NaN at index 0 is never
-// replaced.  One workgroup; ties resolve to the smaller index.
+// replaced.  One workgroup; each thread issues 8 float4 loads per pass before
+// comparing, so a 49152-entry vocabulary is one memory round trip.  Ties
+// resolve to the smaller index.
+__device__ __forceinline__ void arg_better(float v, int i, float &bv, int &bi) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
 __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ x, int n, uint32_t *__restrict__ out) {
+    constexpr int U = 8;
     __shared__ float sv[16];
     __shared__ int si[16];
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = x[i];
-        if (v > bv || (v == bv && i < bi)) {
-            bv = v;
-            bi = i;
+    const int n4 = n >> 2;
+    const f4 *x4 = reinterpret_cast<const f4 *>(x);
+    for (int base = threadIdx.x; base < n4; base += U * 1024) {
+        f4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int c = base + 1024 * u;
+            v[u] = c < n4 ? x4[c] : f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int c = base + 1024 * u;
+            if (c < n4) {
+                arg_better(v[u].x, 4 * c, bv, bi);
+                arg_better(v[u].y, 4 * c + 1, bv, bi);
+                arg_better(v[u].z, 4 * c + 2, bv, bi);
+                arg_better(v[u].w, 4 * c + 3, bv, bi);
+            }
         }
     }
+    for (int i = 4 * n4 + threadIdx.x; i < n; i += 1024) arg_better(x[i], i, bv, bi);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
         const float ov = __shfl_xor(bv, off, 64);
         const int oi = __shfl_xor(bi, off, 64);
-        if (ov > bv || (ov == bv && oi < bi)) {
-            bv = ov;
-            bi = oi;
-        }
+        arg_better(ov, oi, bv, bi);
     }
     const int w = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
@@ -166,11 +221,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int k = 1; k < (int)(blockDim.x >> 6); k++)
-            if (sv[k] > bv || (sv[k] == bv && si[k] < bi)) {
-                bv = sv[k];
-                bi = si[k];
-            }
+        for (int k = 1; k < 16; k++) arg_better(sv[k], si[k], bv, bi);
         // all values NaN (bi unset) or x[0] NaN: wick keeps index 0
         if (bi == 0x7fffffff || isnan(x[0])) bi = 0;
         *out = (uint32_t)bi;
@@ -181,19 +232,25 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
 
 namespace {
 
-template <int NT, int EPI>
-hipError_t gemv_nt(const GemvArgs &a, hipStream_t s) {
-    const dim3 grid((unsigned)((a.rows + 3) / 4), (unsigned)((a.t + NT - 1) / NT)), block(256);
+template <int NT, int R, int UNR, int EPI>
+hipError_t gemv_launch(const GemvArgs &a, hipStream_t s) {
+    const int waves = (a.rows + R - 1) / R;
+    const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)((a.t + NT - 1) / NT)), block(256);
     if (a.norm)
-        hipLaunchKernelGGL((gemv_kernel<NT, EPI, true>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((gemv_kernel<NT, R, UNR, EPI, true>), grid, block, 0, s, a);
     else
-        hipLaunchKernelGGL((gemv_kernel<NT, EPI, false>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((gemv_kernel<NT, R, UNR, EPI, false>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 
+// One token: 8 float4s per lane per pass (rows up to 2048 floats in one pass);
+// the LM head (kEpiStore) takes 4 rows per wave to keep more of its 100+ MB in
+// flight per wave.  Several tokens: 4 per wave, 4 float4s per lane per pass.
 template <int EPI>
 hipError_t gemv_epi(const GemvArgs &a, hipStream_t s) {
-    return a.t == 1 ? gemv_nt<1, EPI>(a, s) : gemv_nt<4, EPI>(a, s);
+    if (a.t > 1) return gemv_launch<4, 1, 4, EPI>(a, s);
+    if constexpr (EPI == kEpiStore) return gemv_launch<1, 4, 4, EPI>(a, s);
+    return gemv_launch<1, 1, 8, EPI>(a, s);
 }
 
 }  // namespace
