@@ -74,9 +74,21 @@ def run_chunks(heads, kv_heads, d, chunks, theta, bias, norm, eps=1e-6, seed=0, 
             start += t
 
 
-def test_qwen3_shape_qk_norm_prefill():
-    # config 3's preparation: QK-norm then RoPE theta 1e6, head_dim 128
-    run_chunks(16, 8, 128, [300], 1e6, bias=False, norm=True)
+def test_qwen3_shape_qk_norm_prefill_then_decode():
+    # config 3's preparation: QK-norm then RoPE theta 1e6, head_dim 128; the
+    # single-token steps run the preparation inside the decode kernel
+    run_chunks(16, 8, 128, [300, 1, 1], 1e6, bias=False, norm=True)
+
+
+def test_decode_prep_with_split_chunks():
+    # len > 192: the decode splits into chunks; only the last chunk's workgroups append
+    run_chunks(14, 2, 64, [700, 1, 1], 1e6, bias=True, norm=True)
+
+
+def test_decode_prep_with_head_slices():
+    # group 20 > 16: two head slices per kv head both prepare (identical) k and v
+    run_chunks(40, 2, 64, [50, 1, 1], 1e4, bias=True, norm=True)
+    run_chunks(40, 2, 64, [300, 1], 1e4, bias=True, norm=True)
 
 
 def test_qwen2_shape_bias_chunked_then_decode():

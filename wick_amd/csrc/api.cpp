@@ -113,6 +113,47 @@ int check_span(const wick_hip_kv *kv, int start, int t) {
     return WICK_HIP_OK;
 }
 
+// Split-K schedule of one decode call over len positions: fills the shape
+// fields of *a and kv->last_grid.
+int plan_decode(wick_hip_kv *kv, int layer, int group, int len, const float *q_dev, float *att_dev,
+                wick::DecodeArgs *a) {
+    const int hslices = (group + wick::kTileRows - 1) / wick::kTileRows;
+    const int units = kv->kv_heads * hslices;
+    int rc = ensure_workspace(kv, units);
+    if (rc) return rc;
+    int chunk = kv->decode_chunk;
+    if (chunk <= 0 && len <= wick::kDecodeSingleChunkMax) {
+        // Short context: one workgroup per unit and no merge pass.  Its 4
+        // waves take at most two 32-key groups each, which costs less
+        // than the second launch a split needs.
+        chunk = len;
+    } else if (chunk <= 0) {
+        // One resident round: as many chunks as the GPU holds decode
+        // workgroups at once, each streaming one long contiguous range.
+        const int resident = kv->num_cus * kv->decode_blocks_per_cu;
+        const int target = std::max(1, resident / units);
+        chunk = (len + target - 1) / target;
+    }
+    chunk = std::max(64, (chunk + 63) / 64 * 64);
+    const int min_chunk = (len + wick::kDecodeMaxChunks - 1) / wick::kDecodeMaxChunks;
+    if (chunk < min_chunk) chunk = (min_chunk + 63) / 64 * 64;
+    const int nchunks = (len + chunk - 1) / chunk;
+    a->q = q_dev;
+    a->k = kv->k_layer(layer);
+    a->v = kv->v_layer(layer);
+    a->att = att_dev;
+    a->part = kv->part;
+    a->capacity = kv->capacity;
+    a->len = len;
+    a->kv_heads = kv->kv_heads;
+    a->group = group;
+    a->hslices = hslices;
+    a->chunk = chunk;
+    a->nchunks = nchunks;
+    kv->last_grid = units * nchunks;
+    return WICK_HIP_OK;
+}
+
 int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int t, int start, float *att_dev) {
     const int D = kv->head_dim;
     if (heads < 1 || heads % kv->kv_heads != 0)
@@ -121,45 +162,11 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
     const float scale = 1.0f / sqrtf((float)D);  // src/model.rs:527
 
     if (t == 1) {
-        const int len = start + 1;
-        const int hslices = (group + wick::kTileRows - 1) / wick::kTileRows;
-        const int units = kv->kv_heads * hslices;
-        int rc = ensure_workspace(kv, units);
-        if (rc) return rc;
-        int chunk = kv->decode_chunk;
-        if (chunk <= 0 && len <= wick::kDecodeSingleChunkMax) {
-            // Short context: one workgroup per unit and no merge pass.  Its 4
-            // waves take at most two 32-key groups each, which costs less
-            // than the second launch a split needs.
-            chunk = len;
-        } else if (chunk <= 0) {
-            // One resident round: as many chunks as the GPU holds decode
-            // workgroups at once, each streaming one long contiguous range.
-            const int resident = kv->num_cus * kv->decode_blocks_per_cu;
-            const int target = std::max(1, resident / units);
-            chunk = (len + target - 1) / target;
-        }
-        chunk = std::max(64, (chunk + 63) / 64 * 64);
-        const int min_chunk = (len + wick::kDecodeMaxChunks - 1) / wick::kDecodeMaxChunks;
-        if (chunk < min_chunk) chunk = (min_chunk + 63) / 64 * 64;
-        const int nchunks = (len + chunk - 1) / chunk;
         wick::DecodeArgs a{};
-        a.q = q_dev;
-        a.k = kv->k_layer(layer);
-        a.v = kv->v_layer(layer);
-        a.att = att_dev;
-        a.part = kv->part;
-        a.capacity = kv->capacity;
-        a.len = len;
-        a.kv_heads = kv->kv_heads;
-        a.group = group;
-        a.hslices = hslices;
-        a.chunk = chunk;
-        a.nchunks = nchunks;
+        int rc = plan_decode(kv, layer, group, start + 1, q_dev, att_dev, &a);
+        if (rc) return rc;
         a.scale = scale;
-        const int grid = units * nchunks;
-        kv->last_grid = grid;
-        hipError_t e = wick::launch_decode(D, a, grid, kv->stream);
+        hipError_t e = wick::launch_decode(D, a, kv->last_grid, kv->stream);
         if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
         return WICK_HIP_OK;
     }
@@ -194,29 +201,49 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
 
 // Bias, QK-norm and RoPE of q (in place) and k, and the append of k and v
 // (src/model.rs:464-484), for tokens at start..start+t of `layer`.
-int run_prep(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev, const float *v_dev, int t,
-             int start) {
+// The registered preparation constants of `layer`, checked against `heads`.
+struct PrepConsts {
+    const float *bq = nullptr, *bk = nullptr, *bv = nullptr, *qn = nullptr, *kn = nullptr;
+    float eps = 0.0f;
+};
+
+int prep_consts(const wick_hip_kv *kv, int layer, int heads, PrepConsts *c) {
     if (!kv->rope_cos) return fail(WICK_HIP_EINVAL, "no RoPE table (call wick_hip_kv_set_rope first)");
     const wick_hip_kv::LayerPrep &p = kv->prep[layer];
     if (!p.set) return fail(WICK_HIP_EINVAL, "layer %d has no preparation constants (call wick_hip_kv_set_prep)", layer);
     if (heads != p.heads)
         return fail(WICK_HIP_EINVAL, "heads %d differs from the %d given to wick_hip_kv_set_prep", heads, p.heads);
     const int D = kv->head_dim, kvd = kv->kv_heads * D;
+    if (p.bias) {
+        c->bq = p.buf;
+        c->bk = p.buf + (size_t)heads * D;
+        c->bv = c->bk + kvd;
+    }
+    if (p.norm) {
+        c->qn = p.buf + (size_t)heads * D + 2 * kvd;
+        c->kn = c->qn + D;
+    }
+    c->eps = p.eps;
+    return WICK_HIP_OK;
+}
+
+int run_prep(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev, const float *v_dev, int t,
+             int start) {
+    PrepConsts c;
+    int rc = prep_consts(kv, layer, heads, &c);
+    if (rc) return rc;
+    const int D = kv->head_dim;
     wick::PrepArgs a{};
     a.q = q_dev;
     a.ksrc = k_dev;
     a.vsrc = v_dev;
     a.k = kv->k_layer(layer);
     a.v = kv->v_layer(layer);
-    if (p.bias) {
-        a.bq = p.buf;
-        a.bk = p.buf + (size_t)heads * D;
-        a.bv = a.bk + kvd;
-    }
-    if (p.norm) {
-        a.qn = p.buf + (size_t)heads * D + 2 * kvd;
-        a.kn = a.qn + D;
-    }
+    a.bq = c.bq;
+    a.bk = c.bk;
+    a.bv = c.bv;
+    a.qn = c.qn;
+    a.kn = c.kn;
     a.rope_cos = kv->rope_cos;
     a.rope_sin = kv->rope_sin;
     a.capacity = kv->capacity;
@@ -224,9 +251,35 @@ int run_prep(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k
     a.t = t;
     a.heads = heads;
     a.kv_heads = kv->kv_heads;
-    a.eps = p.eps;
+    a.eps = c.eps;
     hipError_t e = wick::launch_prep(D, a, kv->stream);
     if (e != hipSuccess) return hip_fail(e, "prep kernel launch");
+    return WICK_HIP_OK;
+}
+
+// One token: the preparation fused into the decode kernel's prologue (q from
+// the raw projections, k and v appended at position start), then attention.
+int run_decode_fused(wick_hip_kv *kv, int layer, int heads, const float *q_raw, const float *k_raw,
+                     const float *v_raw, int start, float *att_dev) {
+    PrepConsts c;
+    int rc = prep_consts(kv, layer, heads, &c);
+    if (rc) return rc;
+    wick::DecodeArgs a{};
+    if ((rc = plan_decode(kv, layer, heads / kv->kv_heads, start + 1, q_raw, att_dev, &a))) return rc;
+    a.scale = 1.0f / sqrtf((float)kv->head_dim);  // src/model.rs:527
+    a.prep = 1;
+    a.kraw = k_raw;
+    a.vraw = v_raw;
+    a.bq = c.bq;
+    a.bk = c.bk;
+    a.bv = c.bv;
+    a.qn = c.qn;
+    a.kn = c.kn;
+    a.rope_cos = kv->rope_cos;
+    a.rope_sin = kv->rope_sin;
+    a.eps = c.eps;
+    hipError_t e = wick::launch_decode(kv->head_dim, a, kv->last_grid, kv->stream);
+    if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
     return WICK_HIP_OK;
 }
 
@@ -242,6 +295,19 @@ int set_error(int code, const char *fmt, ...) {
     va_end(ap);
     g_last_error = buf;
     return code;
+}
+
+int attend_model(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev, const float *v_dev, int t,
+                 int start, float *att_dev) {
+    int rc = check_kv(kv, layer);
+    if (rc) return rc;
+    if ((rc = check_span(kv, start, t))) return rc;
+    if (!q_dev || !k_dev || !v_dev || !att_dev) return fail(WICK_HIP_EINVAL, "null q, k, v or att");
+    if (heads < 1 || heads % kv->kv_heads != 0)
+        return fail(WICK_HIP_EINVAL, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv->kv_heads);
+    if (t == 1) return run_decode_fused(kv, layer, heads, q_dev, k_dev, v_dev, start, att_dev);
+    if ((rc = run_prep(kv, layer, heads, q_dev, k_dev, v_dev, t, start))) return rc;
+    return run_attention(kv, layer, heads, q_dev, t, start, att_dev);
 }
 
 bool kv_info(const wick_hip_kv *kv, KvInfo *out) {
@@ -520,8 +586,8 @@ int wick_hip_attend(wick_hip_kv *kv, int layer, int heads, const float *q, const
     HIP_TRY(hipMemcpyAsync(kv->q_dev, q, nq * sizeof(float), hipMemcpyHostToDevice, kv->stream));
     HIP_TRY(hipMemcpyAsync(kv->kst_dev, k, nk * sizeof(float), hipMemcpyHostToDevice, kv->stream));
     HIP_TRY(hipMemcpyAsync(kv->vst_dev, v, nk * sizeof(float), hipMemcpyHostToDevice, kv->stream));
-    if ((rc = run_prep(kv, layer, heads, kv->q_dev, kv->kst_dev, kv->vst_dev, t, start))) return rc;
-    if ((rc = run_attention(kv, layer, heads, kv->q_dev, t, start, kv->att_dev))) return rc;
+    if ((rc = wick::attend_model(kv, layer, heads, kv->q_dev, kv->kst_dev, kv->vst_dev, t, start, kv->att_dev)))
+        return rc;
     HIP_TRY(hipMemcpyAsync(att, kv->att_dev, nq * sizeof(float), hipMemcpyDeviceToHost, kv->stream));
     HIP_TRY(hipStreamSynchronize(kv->stream));
     return WICK_HIP_OK;

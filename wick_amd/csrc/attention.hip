@@ -245,6 +245,81 @@ __device__ __forceinline__ void init_state(WaveState<D> &st) {
     for (int db = 0; db < Shape<D>::DB; db++) st.o[db] = f4{0.f, 0.f, 0.f, 0.f};
 }
 
+// ------------------------------------------------------------------ fused input preparation
+
+// The per-token preparation of src/model.rs:464-480 for one row of D floats,
+// bit-identical to wick's CPU arithmetic (and to prep_kernel): bias add;
+// rmsnorm_inplace (src/kernels.rs:351-357) -- a sequential f32 sum of squares
+// from -0.0, ss / D, 1 / sqrt(ss + eps) with IEEE divide and square root, then
+// (x * scale) * w; rope (src/model.rs:404-414) -- two rounded products and a
+// rounded sum per output, (sin, cos) from the host-filled table row.
+// 16 lanes own a row: lane l of the group holds the rotation quad j = 4l
+// (< D/2), i.e. elements j..j+3 and j+D/2..j+D/2+3, so all loads go out at
+// once; the sum of squares is carried through the lanes in element order by a
+// chain of shuffles (first half, then second half).  rowbase is the group's
+// first lane; every lane of the group must call this with the same row.
+template <int D>
+__device__ __forceinline__ void prep_row16(const float *src, float *dst, const float *bias, const float *norm,
+                                           float eps, const float *cosr, const float *sinr, int l16, int rowbase) {
+#pragma clang fp contract(off)
+    constexpr int H = D / 2, NQ = H / 4;
+    const bool mine = l16 < NQ;
+    const int j = mine ? 4 * l16 : 0;
+    f4 u = *reinterpret_cast<const f4 *>(src + j), w = *reinterpret_cast<const f4 *>(src + j + H);
+    f4 bu = {0.f, 0.f, 0.f, 0.f}, bw = bu, nu = bu, nw = bu, c = bu, sn = bu;
+    if (bias) {
+        bu = *reinterpret_cast<const f4 *>(bias + j);
+        bw = *reinterpret_cast<const f4 *>(bias + j + H);
+    }
+    if (norm) {
+        nu = *reinterpret_cast<const f4 *>(norm + j);
+        nw = *reinterpret_cast<const f4 *>(norm + j + H);
+    }
+    if (cosr) {
+        c = *reinterpret_cast<const f4 *>(cosr + j);
+        sn = *reinterpret_cast<const f4 *>(sinr + j);
+    }
+    if (bias) {
+        u = u + bu;
+        w = w + bw;
+    }
+    if (norm) {
+        float run = -0.0f;
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            float m = run;
+            m = m + u.x * u.x;
+            m = m + u.y * u.y;
+            m = m + u.z * u.z;
+            m = m + u.w * u.w;
+            run = __shfl(m, rowbase + i, 64);
+        }
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            float m = run;
+            m = m + w.x * w.x;
+            m = m + w.y * w.y;
+            m = m + w.z * w.z;
+            m = m + w.w * w.w;
+            run = __shfl(m, rowbase + i, 64);
+        }
+        run = run / (float)D;
+        const float scale = 1.0f / sqrtf(run + eps);
+        u = u * scale * nu;
+        w = w * scale * nw;
+    }
+    if (cosr) {
+        const f4 a = u * c - w * sn;
+        const f4 b = w * c + u * sn;
+        u = a;
+        w = b;
+    }
+    if (mine) {
+        *reinterpret_cast<f4 *>(dst + j) = u;
+        *reinterpret_cast<f4 *>(dst + j + H) = w;
+    }
+}
+
 // ------------------------------------------------------------------ decode
 
 // Partial states of the split-K decode, per (unit, column): O [units][16][256][D],
@@ -276,11 +351,12 @@ struct DecodeSpace {
 // written directly; otherwise the chunk's (max, sum, O) state per query head
 // goes to the workspace and decode_merge_kernel, the next launch on the
 // stream, combines them (the kernel boundary orders the two).
-template <int D>
+template <int D, bool PREP>
 __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     using S = Shape<D>;
     __shared__ float sm_m[4][16], sm_l[4][16];
     __shared__ float sm_o[4][16][D];
+    __shared__ float sq[PREP ? 16 : 1][D];  // prepared q rows (PREP)
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int units = a.kv_heads * a.hslices;
@@ -294,7 +370,34 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 
     const int col = lane & 15, g = lane >> 4;
     f4 q[S::KJ];
-    load_q<D>(a.q + (size_t)(head0 + col) * D, a.q + (size_t)head0 * D, col < ncols, lane, q);
+    if constexpr (PREP) {
+        // Rows: the unit's ncols q heads (to LDS), then -- in the workgroups
+        // of the last chunk, the only ones that read position len-1 -- the new
+        // k and v rows of the kv head (to the cache).  Workgroups of other
+        // head slices of the same kv head write the same bits there.  The
+        // barrier orders those stores before this workgroup's tile loads.
+        const int pos = a.len - 1;
+        const bool last = chunk == a.nchunks - 1;
+        const int nrows = ncols + (last ? 2 : 0);
+        const float *cr = a.rope_cos + (size_t)pos * (D / 2), *sr = a.rope_sin + (size_t)pos * (D / 2);
+        float *Kw = a.k + ((size_t)kvh * a.capacity + pos) * D;
+        float *Vw = a.v + ((size_t)kvh * a.capacity + pos) * D;
+        for (int r = w * 4 + (lane >> 4); r < nrows; r += 16) {
+            if (r < ncols)
+                prep_row16<D>(a.q + (size_t)(head0 + r) * D, sq[r], a.bq ? a.bq + (size_t)(head0 + r) * D : nullptr, a.qn,
+                              a.eps, cr, sr, lane & 15, lane & 48);
+            else if (r == ncols)
+                prep_row16<D>(a.kraw + (size_t)kvh * D, Kw, a.bk ? a.bk + (size_t)kvh * D : nullptr, a.kn, a.eps, cr, sr,
+                              lane & 15, lane & 48);
+            else
+                prep_row16<D>(a.vraw + (size_t)kvh * D, Vw, a.bv ? a.bv + (size_t)kvh * D : nullptr, nullptr, a.eps,
+                              nullptr, nullptr, lane & 15, lane & 48);
+        }
+        __syncthreads();
+        load_q<D>(sq[col], sq[0], col < ncols, lane, q);
+    } else {
+        load_q<D>(a.q + (size_t)(head0 + col) * D, a.q + (size_t)head0 * D, col < ncols, lane, q);
+    }
 
     WaveState<D> st;
     init_state<D>(st);
@@ -558,17 +661,31 @@ int decode_blocks_per_cu(int head_dim) {
     int n = 0;
     hipError_t e = hipErrorInvalidValue;
     switch (head_dim) {
-    case 16: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<16>, 256, 0); break;
-    case 32: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<32>, 256, 0); break;
-    case 64: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<64>, 256, 0); break;
-    case 128: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<128>, 256, 0); break;
+    case 16: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<16, false>, 256, 0); break;
+    case 32: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<32, false>, 256, 0); break;
+    case 64: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<64, false>, 256, 0); break;
+    case 128: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, decode_kernel<128, false>, 256, 0); break;
     default: break;
     }
     return (e == hipSuccess && n > 0) ? n : 1;
 }
 
+template <int D>
+void launch_decode_d(const DecodeArgs &a, int grid, hipStream_t s) {
+    if (a.prep)
+        hipLaunchKernelGGL((decode_kernel<D, true>), dim3(grid), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((decode_kernel<D, false>), dim3(grid), dim3(256), 0, s, a);
+}
+
 hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_t s) {
-    WICK_DISPATCH_D(head_dim, decode_kernel, dim3(grid), dim3(256), 0, s, a);
+    switch (head_dim) {
+    case 16: launch_decode_d<16>(a, grid, s); break;
+    case 32: launch_decode_d<32>(a, grid, s); break;
+    case 64: launch_decode_d<64>(a, grid, s); break;
+    case 128: launch_decode_d<128>(a, grid, s); break;
+    default: return hipErrorInvalidValue;
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nchunks == 1) return e;
     const int units = a.kv_heads * a.hslices;

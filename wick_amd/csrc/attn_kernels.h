@@ -16,13 +16,21 @@ constexpr int kDecodeSingleChunkMax = 192;
 constexpr int kTileRows = 16;  // query rows (or heads) per MFMA column block
 
 struct DecodeArgs {
-    const float *q;   // [heads*D] (one token)
-    const float *k;   // layer base, [kv_heads][capacity][D]
-    const float *v;
+    const float *q;   // [heads*D] (one token); raw projections when prep != 0
+    float *k;         // layer base, [kv_heads][capacity][D]
+    float *v;
     float *att;       // [heads*D]
     float *part;      // partial states, see decode_workspace_floats
     int capacity, len, kv_heads, group, hslices, chunk, nchunks;
     float scale;
+    // Fused input preparation (prep != 0): q is raw; kraw / vraw [kv_heads*D]
+    // are the new token's raw k and v, prepared and appended at position len-1
+    // by the workgroups that own the last chunk.  Biases / norms may be null.
+    int prep;
+    const float *kraw, *vraw;
+    const float *bq, *bk, *bv, *qn, *kn;
+    const float *rope_cos, *rope_sin;  // [capacity][D/2] tables
+    float eps;
 };
 
 struct PrefillArgs {
@@ -72,6 +80,12 @@ struct KvInfo {
     hipStream_t stream;
 };
 bool kv_info(const wick_hip_kv *kv, KvInfo *out);
+
+// src/model.rs:464-485 for one layer on device arrays, as wick_hip_attend_device
+// except that q_dev is scratch (its contents afterwards are unspecified): for
+// one token the preparation runs in the decode kernel's prologue.
+int attend_model(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev, const float *v_dev, int t,
+                 int start, float *att_dev);
 
 // Record the message wick_hip_last_error() returns on this thread; returns code.
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));

@@ -4,7 +4,8 @@
 //
 // Per layer and chunk of t tokens the stream runs:
 //   gemv  attn_norm + [wq; wk; wv]   -> q, k, v       (src/model.rs:449-462)
-//   wick_hip_attend_device: bias, QK-norm, RoPE, cache append, attention (:464-485)
+//   attend_model: bias, QK-norm, RoPE, cache append, attention (:464-485); for
+//                 one token the preparation is the decode kernel's prologue
 //   gemv  wo, residual add into x                      (:486-487)
 //   gemv  ffn_norm + w_gate, w_up, silu_mul -> h       (:490-501)
 //   gemv  w_down, residual add into x                  (:502-503)
@@ -180,7 +181,7 @@ int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, 
         g.t = t;
         if ((e = wick::launch_gemv(wick::kEpiQkv, g, s)) != hipSuccess) return hip_fail(e, "qkv gemv launch");
 
-        RC_TRY(wick_hip_attend_device(kv, li, c.heads, m->q, m->k, m->v, t, start, m->att));
+        RC_TRY(wick::attend_model(kv, li, c.heads, m->q, m->k, m->v, t, start, m->att));
 
         g = wick::GemvArgs{};
         g.x = m->att;
