@@ -212,6 +212,61 @@ def measure_long_decode(torch, kv_cls, native, dev, steps):
             "bytes_per_layer": bytes_layer, "auto": best, "chunk_sweep": sweep}
 
 
+def measure_e2e():
+    """configs[0] through wick's cmd_bench loop (src/main.rs:223-258): prefill a 128-token
+    prompt, then 64 greedy single-token forwards; decode tok/s = forwards / wall time."""
+    import numpy as np
+    from wick_amd.device_model import DeviceModel
+    from wick_amd.host import HostModel
+    from wick_amd.synthetic import random_prompt, random_weights, smollm2_135m
+    cfg = smollm2_135m()
+    w = random_weights(cfg, seed=0)
+    prompt = random_prompt(1, 128, cfg.vocab)
+    n_gen = 64
+    # (1) the drop-in: wick's host forward (C++ mirror, projections on the CPU),
+    #     with the per-layer preparation, KV cache and attention on the GPU
+    hm = HostModel(cfg, w)
+    st = hm.new_state(128 + n_gen + 8)
+    hm.forward(st, prompt[:8])  # warm the pool and the device path, as cmd_bench does
+    st.len = 0
+    t0 = time.perf_counter()
+    logits = hm.forward(st, prompt)
+    t1 = time.perf_counter()
+    tok = int(np.argmax(logits[0]))
+    host_ids = [tok]
+    for _ in range(n_gen):
+        logits = hm.forward(st, [tok])
+        tok = int(np.argmax(logits[0]))
+        host_ids.append(tok)
+    t2 = time.perf_counter()
+    host = {"prompt_tok_s": round(128 / (t1 - t0), 1), "decode_tok_s": round(n_gen / (t2 - t1), 2),
+            "host_threads": os.cpu_count()}
+    hm.close()
+    # (2) the whole forward resident on the GPU: projections, norms, SwiGLU, LM head
+    #     and the greedy argmax; ids stay on the device between steps
+    dm = DeviceModel(cfg, w)
+    best = None
+    for rep in range(3):  # rep 0 warms up allocations and code objects
+        cache = dm.new_cache(128 + n_gen + 8)
+        t0 = time.perf_counter()
+        first = dm.prefill(cache, prompt)
+        t1 = time.perf_counter()
+        ids = [first] + dm.decode(cache, first, n_gen)
+        t2 = time.perf_counter()
+        cache.close()
+        if rep and (best is None or t2 - t1 < best[1]):
+            best = (t1 - t0, t2 - t1, ids)
+    dm.close()
+    del w
+    return {"workload": f"random-init SmolLM2-135M architecture, f32, 128-token prompt + {n_gen} greedy "
+                        "tokens (wick's cmd_bench loop: decode tok/s = single-token forwards / wall time)",
+            "device_resident": {"prompt_tok_s": round(128 / best[0], 1),
+                                "decode_tok_s": round(n_gen / best[1], 2),
+                                "ms_per_token": round(best[1] * 1e3 / n_gen, 3)},
+            "host_forward_gpu_attention": host,
+            "greedy_ids_identical": best[2] == host_ids}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -220,6 +275,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--e2e-only", action="store_true", help="run only the e2e leg (configs[0]) and print its JSON")
     ap.add_argument("--no-long", action="store_true", help="skip configs[4] (16 GiB long-context decode)")
     ap.add_argument("--pmc-case", nargs="?", const="decode", choices=["decode", "prefill"],
                     help="short fixed workload for rocprofv3 --pmc runs: 'decode' = 24 decode calls (one per layer) "
@@ -242,6 +298,10 @@ def main():
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     c = DEC
+
+    if args.e2e_only:
+        print(json.dumps(measure_e2e()), flush=True)
+        return
 
     if args.pmc_case == "prefill":
         measure_prefill(torch, DeviceKvCache, dev, PRE["heads"], PRE["kv_heads"], PRE["d"], PRE["T"], 0,
@@ -344,57 +404,9 @@ def main():
 
     # ---------------- e2e: wick's cmd_bench loop (src/main.rs:223-258)
     if not args.no_e2e:
-        import numpy as np
-        from wick_amd.device_model import DeviceModel
-        from wick_amd.host import HostModel
-        from wick_amd.synthetic import random_prompt, random_weights, smollm2_135m
-        cfg = smollm2_135m()
-        w = random_weights(cfg, seed=0)
-        prompt = random_prompt(1, 128, cfg.vocab)
-        n_gen = 64
-        # (1) the drop-in: wick's host forward (C++ mirror, projections on the CPU),
-        #     with the per-layer preparation, KV cache and attention on the GPU
-        hm = HostModel(cfg, w)
-        st = hm.new_state(128 + n_gen + 8)
-        hm.forward(st, prompt[:8])  # warm the pool and the device path, as cmd_bench does
-        st.len = 0
-        t0 = time.perf_counter()
-        logits = hm.forward(st, prompt)
-        t1 = time.perf_counter()
-        tok = int(np.argmax(logits[0]))
-        host_ids = [tok]
-        for _ in range(n_gen):
-            logits = hm.forward(st, [tok])
-            tok = int(np.argmax(logits[0]))
-            host_ids.append(tok)
-        t2 = time.perf_counter()
-        host = {"prompt_tok_s": round(128 / (t1 - t0), 1), "decode_tok_s": round(n_gen / (t2 - t1), 2),
-                "host_threads": os.cpu_count()}
-        hm.close()
-        # (2) the whole forward resident on the GPU: projections, norms, SwiGLU, LM head
-        #     and the greedy argmax; ids stay on the device between steps
-        dm = DeviceModel(cfg, w)
-        best = None
-        for rep in range(3):  # rep 0 warms up allocations and code objects
-            cache = dm.new_cache(128 + n_gen + 8)
-            t0 = time.perf_counter()
-            first = dm.prefill(cache, prompt)
-            t1 = time.perf_counter()
-            ids = [first] + dm.decode(cache, first, n_gen)
-            t2 = time.perf_counter()
-            cache.close()
-            if rep and (best is None or t2 - t1 < best[1]):
-                best = (t1 - t0, t2 - t1, ids)
-        dm.close()
-        del w
-        out["e2e_decode_tok_s"] = round(n_gen / best[1], 2)
-        out["e2e"] = {"workload": f"random-init SmolLM2-135M architecture, f32, 128-token prompt + {n_gen} greedy "
-                                  "tokens (wick's cmd_bench loop: decode tok/s = single-token forwards / wall time)",
-                      "device_resident": {"prompt_tok_s": round(128 / best[0], 1),
-                                          "decode_tok_s": round(n_gen / best[1], 2),
-                                          "ms_per_token": round(best[1] * 1e3 / n_gen, 3)},
-                      "host_forward_gpu_attention": host,
-                      "greedy_ids_identical": best[2] == host_ids}
+        e2e = measure_e2e()
+        out["e2e_decode_tok_s"] = e2e["device_resident"]["decode_tok_s"]
+        out["e2e"] = e2e
 
     # ---------------- CPU baseline (oracle on the host cores, bounded sample)
     if not args.no_cpu:
