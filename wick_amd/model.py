@@ -121,15 +121,17 @@ class Config:
 
 
 def load_safetensors(path):
-    """name -> float32 ndarray (bf16 and f16 widened exactly)."""
-    with open(path, "rb") as f:
-        raw = f.read()
-    if len(raw) < 8:
+    """name -> float32 ndarray, read through a memory map (src/safetensors.rs:56-118 maps
+    the file too).  F32 tensors are views of the mapped pages, so handing them to
+    wick_hip_model_create copies them from the page cache straight into HBM without
+    a host copy; bf16 and f16 are widened exactly into new arrays."""
+    mm = np.memmap(path, dtype=np.uint8, mode="r")
+    if mm.size < 8:
         raise ValueError("file too short")
-    (hlen,) = struct.unpack("<Q", raw[:8])
-    if hlen > len(raw) - 8:
+    hlen = int(np.frombuffer(mm[:8].tobytes(), "<u8")[0])
+    if hlen > mm.size - 8:
         raise ValueError("bad header length")
-    header = json.loads(raw[8:8 + hlen].decode("utf-8"))
+    header = json.loads(mm[8:8 + hlen].tobytes().decode("utf-8"))
     base = 8 + hlen
     out = {}
     for name, info in header.items():
@@ -142,15 +144,15 @@ def load_safetensors(path):
         size = {"F32": 4, "BF16": 2, "F16": 2}.get(dt)
         if size is None:
             raise ValueError(f"{name}: unsupported dtype {dt}")
-        if e < b or base + e > len(raw) or e - b != n * size:
+        if e < b or base + e > mm.size or e - b != n * size:
             raise ValueError(f"{name}: data range does not match its shape")
-        buf = raw[base + b:base + e]
+        buf = mm[base + b:base + e]
         if dt == "F32":
-            a = np.frombuffer(buf, "<f4").astype(np.float32)
+            a = buf.view("<f4") if (base + b) % 4 == 0 else np.frombuffer(buf.tobytes(), "<f4")
         elif dt == "BF16":
-            a = (np.frombuffer(buf, "<u2").astype(np.uint32) << 16).view(np.float32)
+            a = (buf.view("<u2").astype(np.uint32) << 16).view(np.float32)
         else:
-            a = np.frombuffer(buf, "<f2").astype(np.float32)
+            a = buf.view("<f2").astype(np.float32)
         out[name] = a.reshape(shape)
     return out
 
