@@ -124,7 +124,7 @@ struct WaveState {
     f4 o[Shape<D>::DB];
 };
 
-template <int D>
+template <int D, int CHAINS = 2>
 __device__ __forceinline__ void compute_tiles(const TileBuf<D> &b, int kbeg, int first, int klimit, float scale,
                                               const f4 (&q)[Shape<D>::KJ], int lane, WaveState<D> &st) {
     using S = Shape<D>;
@@ -133,16 +133,24 @@ __device__ __forceinline__ void compute_tiles(const TileBuf<D> &b, int kbeg, int
     float mloc = -INFINITY;
 #pragma unroll
     for (int u = 0; u < S::TG; u++) {
-        f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+        // CHAINS independent accumulator chains (fewer if KJ is smaller),
+        // interleaved so that consecutive MFMAs do not wait on each other's
+        // results; more chains cost registers.
+        constexpr int NCH = S::KJ < CHAINS ? S::KJ : CHAINS;
+        f4 sch[NCH];
 #pragma unroll
-        for (int j = 0; j < S::KJ; j++) {
+        for (int c = 0; c < NCH; c++) sch[c] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jj = 0; jj < S::KJ; jj += NCH) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                if (j & 1) s1 = mfma16x16x4(b.k[u][j][e], q[j][e], s1);
-                else       s0 = mfma16x16x4(b.k[u][j][e], q[j][e], s0);
+#pragma unroll
+                for (int c = 0; c < NCH; c++) sch[c] = mfma16x16x4(b.k[u][jj + c][e], q[jj + c][e], sch[c]);
             }
         }
-        const f4 s = s0 + s1;
+        f4 s = sch[0];
+#pragma unroll
+        for (int c = 1; c < NCH; c++) s += sch[c];
         const int key0 = kbeg + 16 * (first + u) + 4 * g;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -190,7 +198,7 @@ __device__ __forceinline__ void compute_tiles(const TileBuf<D> &b, int kbeg, int
 // the next group are issued before the current group is computed (PINGPONG),
 // or each group is loaded then computed with half the registers, which buys
 // more resident waves instead (the better trade for head_dim 128 decode).
-template <int D, bool PINGPONG = true>
+template <int D, bool PINGPONG = true, int CHAINS = 2>
 __device__ __forceinline__ void attend_range(const float *__restrict__ Kh, const float *__restrict__ Vh, int kbeg,
                                              int kend, int tile0, int tstep, int klimit, float scale,
                                              const f4 (&q)[Shape<D>::KJ], int lane, WaveState<D> &st) {
@@ -200,7 +208,7 @@ __device__ __forceinline__ void attend_range(const float *__restrict__ Kh, const
         TileBuf<D> b;
         for (int first = tile0; first < ntiles; first += tstep) {
             load_tiles<D>(Kh, Vh, kbeg, kend, first, lane, b);
-            compute_tiles<D>(b, kbeg, first, klimit, scale, q, lane, st);
+            compute_tiles<D, CHAINS>(b, kbeg, first, klimit, scale, q, lane, st);
         }
         return;
     }
@@ -211,12 +219,12 @@ __device__ __forceinline__ void attend_range(const float *__restrict__ Kh, const
     for (;;) {
         int next = first + tstep;
         if (next < ntiles) load_tiles<D>(Kh, Vh, kbeg, kend, next, lane, bb);
-        compute_tiles<D>(ba, kbeg, first, klimit, scale, q, lane, st);
+        compute_tiles<D, CHAINS>(ba, kbeg, first, klimit, scale, q, lane, st);
         first = next;
         if (first >= ntiles) break;
         next = first + tstep;
         if (next < ntiles) load_tiles<D>(Kh, Vh, kbeg, kend, next, lane, ba);
-        compute_tiles<D>(bb, kbeg, first, klimit, scale, q, lane, st);
+        compute_tiles<D, CHAINS>(bb, kbeg, first, klimit, scale, q, lane, st);
         first = next;
         if (first >= ntiles) break;
     }
@@ -569,7 +577,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
 // wave's softmax with another's MFMAs.  The wave holding key 0 -- valid for
 // every row -- keeps each merged max finite.
 template <int D>
-__global__ __launch_bounds__(256) void prefill_split_kernel(const PrefillArgs a) {
+__device__ __forceinline__ void prefill_split_body(const PrefillArgs &a) {
     using S = Shape<D>;
     __shared__ float sm_m[4][16], sm_l[4][16];
     __shared__ float sm_o[4][16][D];
@@ -594,7 +602,7 @@ __global__ __launch_bounds__(256) void prefill_split_kernel(const PrefillArgs a)
     load_q<D>(a.q + (size_t)i * heads * D + (size_t)(kvh * a.group + hh) * D, a.q, valid, lane, q);
     WaveState<D> st;
     init_state<D>(st);
-    attend_range<D, (D < 128)>(Kh, Vh, ks, ke, 0, S::TG, lim, a.scale, q, lane, st);
+    attend_range<D, (D < 128), 4>(Kh, Vh, ks, ke, 0, S::TG, lim, a.scale, q, lane, st);
     st.l = col_sum(st.l);
     if (g == 0) {
         sm_m[w][col] = st.m;
@@ -623,6 +631,17 @@ __global__ __launch_bounds__(256) void prefill_split_kernel(const PrefillArgs a)
         const int ic = rc / a.group, hc = rc % a.group;
         a.att[(size_t)ic * heads * D + (size_t)(kvh * a.group + hc) * D + d] = o / L;
     }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void prefill_split_kernel(const PrefillArgs a) {
+    prefill_split_body<D>(a);
+}
+
+// head_dim 128 held to 3 waves per SIMD (at most 168 VGPRs)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prefill_split_kernel_d128(
+    const PrefillArgs a) {
+    prefill_split_body<128>(a);
 }
 
 // ------------------------------------------------------------------ append
@@ -700,7 +719,9 @@ int prefill_grid(const PrefillArgs &a) {
 
 hipError_t launch_prefill(int head_dim, const PrefillArgs &a, hipStream_t s) {
     const int grid = prefill_grid(a);
-    if (a.split) {
+    if (a.split && head_dim == 128) {
+        hipLaunchKernelGGL(prefill_split_kernel_d128, dim3(grid), dim3(256), 0, s, a);
+    } else if (a.split) {
         WICK_DISPATCH_D(head_dim, prefill_split_kernel, dim3(grid), dim3(256), 0, s, a);
     } else {
         WICK_DISPATCH_D(head_dim, prefill_kernel, dim3(grid), dim3(256), 0, s, a);
