@@ -55,15 +55,29 @@ __device__ __forceinline__ f4 mfma16x16x4(float a, float b, f4 c) {
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// max / sum over the four lanes that hold the same column (l, l^16, l^32, l^48)
-__device__ __forceinline__ float col_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16));
-    return fmaxf(v, __shfl_xor(v, 32));
+// max / sum over the four lanes that hold the same column (l, l^16, l^32, l^48).
+// v_permlane16_swap / v_permlane32_swap (gfx950) hand each lane the pair
+// {v[l], v[l^16]} / {v[l], v[l^32]} in a VALU op (checked on the device), so the
+// column reduction needs no LDS round trip; a max or sum of the pair equals the
+// xor-shuffle step bit for bit.
+__device__ __forceinline__ float xor16_pair_max(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
-__device__ __forceinline__ float col_sum(float v) {
-    v += __shfl_xor(v, 16);
-    return v + __shfl_xor(v, 32);
+__device__ __forceinline__ float xor32_pair_max(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
+__device__ __forceinline__ float xor16_pair_sum(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float xor32_pair_sum(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float col_max(float v) { return xor32_pair_max(xor16_pair_max(v)); }
+__device__ __forceinline__ float col_sum(float v) { return xor32_pair_sum(xor16_pair_sum(v)); }
 
 template <int W>
 __device__ __forceinline__ void load_w(const float *p, float *out) {
