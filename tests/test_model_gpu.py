@@ -141,6 +141,30 @@ def test_prefill_chunks_of_256():
     assert nxt == ol.argmax(want)
 
 
+@pytest.mark.parametrize("name", MODELS)
+def test_decode_across_the_split_threshold(name):
+    """Decode steps at 180..210 positions: single-chunk decode, then split-K + merge, both
+    with the preparation in the decode kernel's prologue; logits and ids against the CPU."""
+    cfg, w, exp = fixture(name)
+    rng = np.random.default_rng(11)
+    prompt = [int(x) for x in rng.integers(0, cfg.vocab, 180)]
+    om = ol.OracleModel(cfg, w)
+    ost = om.new_state(256)
+    want = om.forward(ost, prompt)
+    with DeviceModel(cfg, w) as m:
+        cache = m.new_cache(256)
+        got = m.forward(cache, prompt)
+        for step in range(30):
+            assert np.abs(got[0] - want[0]).max() < 1e-4, f"{name}: step {step}"
+            tok = ol.argmax(want[0])
+            assert int(np.argmax(got[0])) == tok
+            got = m.forward(cache, [tok])
+            want = om.forward(ost, [tok])
+        k_gpu, v_gpu = cache.read(cfg.layers - 1, 0, 210)
+    k_cpu = ost["k"][cfg.layers - 1, :210]
+    assert np.abs(k_gpu - k_cpu).max() < 1e-4
+
+
 def test_model_errors():
     cfg, w, exp = fixture("llama3-scaled-f32")
     with DeviceModel(cfg, w) as m:
