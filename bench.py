@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X attention path (one JSON line on stdout).
 
-Workload: decode attention, Qwen2.5-0.5B shape --
+Workload (the headline configuration): decode attention, Qwen2.5-0.5B shape --
 14 query heads / 2 KV heads, head_dim 64, f32, 24 layers, one new query token
 per layer over a KV cache of 32768 positions per layer.  One step = the decode
 attention of all 24 layers (24 launches, one per layer, each over its own
@@ -10,9 +10,10 @@ the 256 MB Infinity Cache).  Inputs are resident in HBM before timing starts.
 
 value  = algorithmic bytes per step / step time, in GB/s, where one layer
          reads 4*(2*L*Hkv*d + 2*Hq*d) bytes (K, V, q, and writes att).
-Also reported: causal prefill TFLOP/s (configs[2], Qwen3 shape, T = 512 and
-2048), chunked prefill, long-context decode with a split-K chunk
-sweep, e2e decode tok/s and the CPU oracle timed on
+Also reported: causal prefill TFLOP/s (Qwen3 shape, T = 512 and 2048), chunked
+prefill (TinyLlama shape, 512 tokens onto 1536 cached), long-context decode with
+a split-K chunk sweep (Llama-3-8B shape, 65536 positions), e2e decode tok/s
+(SmolLM2-135M architecture, wick's cmd_bench loop) and the CPU oracle timed on
 the host cores on a bounded sample (cpu_baseline).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -286,7 +287,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(sharding is described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(attention would shard by kv head, or by sequence with one log-sum-exp merge). "
+              "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -1,6 +1,6 @@
 """Synthetic models and inputs for the benchmark configurations (no checkpoints are available offline).
 
-smollm2_135m() is the architecture of BASELINE configs[0]: Llama, 30 layers,
+smollm2_135m() is the SmolLM2-135M architecture of the e2e benchmark: Llama, 30 layers,
 hidden 576, 9 query / 3 KV heads, head_dim 64, FFN 1536 SiLU-gated, RMSNorm eps
 1e-5, RoPE theta 10000, vocab 49152, tied embeddings.  Matrices are f32
 N(0, 0.02) drawn with numpy's PCG64 from the given seed, in a fixed order;
