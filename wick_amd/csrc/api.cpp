@@ -76,9 +76,14 @@ struct wick_hip_kv {
 
 namespace {
 
-int grow(float **buf, size_t *cap, size_t need, const char *what) {
+int grow(hipStream_t stream, float **buf, size_t *cap, size_t need, const char *what) {
     if (need <= *cap) return WICK_HIP_OK;
-    if (*buf) (void)hipFree(*buf);
+    // work queued earlier on the handle's stream may still read the old buffer
+    if (*buf) {
+        hipError_t e = hipStreamSynchronize(stream);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+        (void)hipFree(*buf);
+    }
     *buf = nullptr;
     *cap = 0;
     hipError_t e = hipMalloc(buf, need * sizeof(float));
@@ -91,7 +96,10 @@ int grow(float **buf, size_t *cap, size_t need, const char *what) {
 // demand; a decode launch rewrites every state it later reads.
 int ensure_workspace(wick_hip_kv *kv, int units) {
     if (units <= kv->ws_units) return WICK_HIP_OK;
-    if (kv->part) (void)hipFree(kv->part);
+    if (kv->part) {
+        HIP_TRY(hipStreamSynchronize(kv->stream));  // an earlier decode may still use it
+        (void)hipFree(kv->part);
+    }
     kv->part = nullptr;
     kv->ws_units = 0;
     HIP_TRY(hipMalloc(&kv->part, wick::decode_workspace_floats(units, kv->head_dim) * sizeof(float)));
@@ -434,8 +442,8 @@ int wick_hip_kv_append(wick_hip_kv *kv, int layer, int start, int t, const float
     if (n > kv->kst_cap) {
         size_t ck = kv->kst_cap, cv = kv->kst_cap;
         kv->kst_cap = 0;
-        if ((rc = grow(&kv->kst_dev, &ck, n, "hipMalloc(k staging)"))) return rc;
-        if ((rc = grow(&kv->vst_dev, &cv, n, "hipMalloc(v staging)"))) return rc;
+        if ((rc = grow(kv->stream, &kv->kst_dev, &ck, n, "hipMalloc(k staging)"))) return rc;
+        if ((rc = grow(kv->stream, &kv->vst_dev, &cv, n, "hipMalloc(v staging)"))) return rc;
         kv->kst_cap = n;
     }
     HIP_TRY(hipMemcpyAsync(kv->kst_dev, k, n * sizeof(float), hipMemcpyHostToDevice, kv->stream));
@@ -479,8 +487,8 @@ int wick_hip_attention(wick_hip_kv *kv, int layer, int heads, const float *q, in
     if (!q || !att) return fail(WICK_HIP_EINVAL, "null q or att");
     if (heads < 1) return fail(WICK_HIP_EINVAL, "heads must be >= 1");
     const size_t n = (size_t)t * heads * kv->head_dim;
-    if ((rc = grow(&kv->q_dev, &kv->q_cap, n, "hipMalloc(q staging)"))) return rc;
-    if ((rc = grow(&kv->att_dev, &kv->att_cap, n, "hipMalloc(att staging)"))) return rc;
+    if ((rc = grow(kv->stream, &kv->q_dev, &kv->q_cap, n, "hipMalloc(q staging)"))) return rc;
+    if ((rc = grow(kv->stream, &kv->att_dev, &kv->att_cap, n, "hipMalloc(att staging)"))) return rc;
     HIP_TRY(hipMemcpyAsync(kv->q_dev, q, n * sizeof(float), hipMemcpyHostToDevice, kv->stream));
     if ((rc = run_attention(kv, layer, heads, kv->q_dev, t, start, kv->att_dev))) return rc;
     HIP_TRY(hipMemcpyAsync(att, kv->att_dev, n * sizeof(float), hipMemcpyDeviceToHost, kv->stream));
@@ -574,13 +582,13 @@ int wick_hip_attend(wick_hip_kv *kv, int layer, int heads, const float *q, const
     if (heads < 1 || heads % kv->kv_heads != 0)
         return fail(WICK_HIP_EINVAL, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv->kv_heads);
     const size_t nq = (size_t)t * heads * kv->head_dim, nk = (size_t)t * kv->kv_heads * kv->head_dim;
-    if ((rc = grow(&kv->q_dev, &kv->q_cap, nq, "hipMalloc(q staging)"))) return rc;
-    if ((rc = grow(&kv->att_dev, &kv->att_cap, nq, "hipMalloc(att staging)"))) return rc;
+    if ((rc = grow(kv->stream, &kv->q_dev, &kv->q_cap, nq, "hipMalloc(q staging)"))) return rc;
+    if ((rc = grow(kv->stream, &kv->att_dev, &kv->att_cap, nq, "hipMalloc(att staging)"))) return rc;
     if (nk > kv->kst_cap) {
         size_t ck = kv->kst_cap, cv = kv->kst_cap;
         kv->kst_cap = 0;
-        if ((rc = grow(&kv->kst_dev, &ck, nk, "hipMalloc(k staging)"))) return rc;
-        if ((rc = grow(&kv->vst_dev, &cv, nk, "hipMalloc(v staging)"))) return rc;
+        if ((rc = grow(kv->stream, &kv->kst_dev, &ck, nk, "hipMalloc(k staging)"))) return rc;
+        if ((rc = grow(kv->stream, &kv->vst_dev, &cv, nk, "hipMalloc(v staging)"))) return rc;
         kv->kst_cap = nk;
     }
     HIP_TRY(hipMemcpyAsync(kv->q_dev, q, nq * sizeof(float), hipMemcpyHostToDevice, kv->stream));
