@@ -160,6 +160,123 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
     }
 }
 
+// Several tokens (prompt chunks): out rows of W . X^T on the f32 matrix cores.
+// A workgroup computes 16 output rows x 16*TB tokens as TB accumulators of
+// v_mfma_f32_16x16x4_f32 (A = 16 weight rows x 4 k, B = 4 k x 16 tokens); the
+// contraction index is permuted so each lane loads whole float4s: MFMA e of
+// k-step s uses k = 16s + 4*(lane/16) + e for both operands.  Lane l then holds
+// rows row0 + 4*(l/16) + r of token tok0 + 16b + l%16.  The input rows are
+// already normalised (rmsnorm_kernel); the epilogues are gemv_kernel's.
+__device__ __forceinline__ f4 mfma4(float a, float b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+
+template <int EPI, int TB>
+__global__ __launch_bounds__(256) void gemm_kernel(const GemvArgs a) {
+    // workgroup = one tile of 16 rows x 16*TB tokens; its 4 waves split k in
+    // four contiguous ranges and their partial tiles are summed through LDS
+    __shared__ f4 red[3][TB][2][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int row0 = 16 * blockIdx.x;
+    const int tok0 = blockIdx.y * 16 * TB;
+    const int i = lane & 15, g = lane >> 4;
+    const float *wr = a.w + (size_t)min(row0 + i, a.rows - 1) * a.cols + 4 * g;
+    const float *w2r = EPI == kEpiSwiglu ? a.w2 + (size_t)min(row0 + i, a.rows - 1) * a.cols + 4 * g : wr;
+    const float *xr[TB];
+#pragma unroll
+    for (int b = 0; b < TB; b++) xr[b] = a.x + (size_t)min(tok0 + 16 * b + i, a.t - 1) * a.cols + 4 * g;
+    f4 acc[TB], acc2[TB];
+#pragma unroll
+    for (int b = 0; b < TB; b++) acc[b] = acc2[b] = f4{0.f, 0.f, 0.f, 0.f};
+    auto step = [&](const f4 &wv, const f4 &w2v, const f4 (&xv)[TB]) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+#pragma unroll
+            for (int b = 0; b < TB; b++) {
+                acc[b] = mfma4(wv[e], xv[b][e], acc[b]);
+                if (EPI == kEpiSwiglu) acc2[b] = mfma4(w2v[e], xv[b][e], acc2[b]);
+            }
+        }
+    };
+    // this wave's k range, in 16-wide steps
+    const int steps = a.cols / 16;
+    const int s0 = (w * steps) >> 2, s1 = ((w + 1) * steps) >> 2;
+    constexpr int KU = 4;  // steps per load batch: all of a batch's loads go out together
+    for (int st = s0; st < s1; st += KU) {
+        f4 wv[KU], w2v[KU], xv[KU][TB];
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int k = 16 * min(st + u, s1 - 1);
+            wv[u] = *reinterpret_cast<const f4 *>(wr + k);
+            w2v[u] = wv[u];
+            if (EPI == kEpiSwiglu) w2v[u] = *reinterpret_cast<const f4 *>(w2r + k);
+#pragma unroll
+            for (int b = 0; b < TB; b++) xv[u][b] = *reinterpret_cast<const f4 *>(xr[b] + k);
+        }
+#pragma unroll
+        for (int u = 0; u < KU; u++)
+            if (st + u < s1) step(wv[u], w2v[u], xv[u]);
+    }
+    if (w > 0) {
+#pragma unroll
+        for (int b = 0; b < TB; b++) {
+            red[w - 1][b][0][lane] = acc[b];
+            if (EPI == kEpiSwiglu) red[w - 1][b][1][lane] = acc2[b];
+        }
+    }
+    __syncthreads();
+    if (w > 0) return;
+#pragma unroll
+    for (int b = 0; b < TB; b++) {
+#pragma unroll
+        for (int ww = 0; ww < 3; ww++) {
+            acc[b] += red[ww][b][0][lane];
+            if (EPI == kEpiSwiglu) acc2[b] += red[ww][b][1][lane];
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < TB; b++) {
+        const int tok = tok0 + 16 * b + i;
+        if (tok >= a.t) continue;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = row0 + 4 * g + r;
+            if (row >= a.rows) continue;
+            const float d = acc[b][r];
+            const size_t t = (size_t)tok;
+            if (EPI == kEpiStore) {
+                a.out0[t * a.ld0 + row] = d;
+            } else if (EPI == kEpiResid) {
+                a.out0[t * a.ld0 + row] += d;
+            } else if (EPI == kEpiQkv) {
+                if (row < a.split0)
+                    a.out0[t * a.ld0 + row] = d;
+                else if (row < a.split1)
+                    a.out1[t * a.ld1 + (row - a.split0)] = d;
+                else
+                    a.out2[t * a.ld2 + (row - a.split1)] = d;
+            } else {
+                a.out0[t * a.ld0 + row] = d / (1.0f + expf(-d)) * acc2[b][r];
+            }
+        }
+    }
+}
+
+// rmsnorm (src/kernels.rs:343-349) of t rows of n floats: one workgroup per row,
+// a fixed-order reduction, xn = x * scale * g.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ g,
+                                                      float eps, float *__restrict__ out, int n) {
+    __shared__ float red[4];
+    const float *xr = x + (size_t)blockIdx.x * n;
+    float ss = 0.0f;
+    for (int c = threadIdx.x; c < n; c += 256) ss = fmaf(xr[c], xr[c], ss);
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+    float *o = out + (size_t)blockIdx.x * n;
+    for (int c = threadIdx.x; c < n; c += 256) o[c] = xr[c] * scale * g[c];
+}
+
 __global__ __launch_bounds__(256) void embed_kernel(const float *__restrict__ embed, const uint32_t *__restrict__ tokens,
                                                     float *__restrict__ x, int hidden) {
     const int i = blockIdx.x;
@@ -264,6 +381,27 @@ hipError_t launch_gemv(int epi, const GemvArgs &a, hipStream_t s) {
     case kEpiSwiglu: return gemv_epi<kEpiSwiglu>(a, s);
     default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemm(int epi, const GemvArgs &a, hipStream_t s) {
+    if (a.rows <= 0 || a.t <= 0) return hipSuccess;
+    if (a.cols % 16 != 0 || a.norm) return hipErrorInvalidValue;
+    constexpr int TB = 2;  // 32 tokens per workgroup tile
+    const dim3 grid((unsigned)((a.rows + 15) / 16), (unsigned)((a.t + 16 * TB - 1) / (16 * TB))), block(256);
+    switch (epi) {
+    case kEpiStore: hipLaunchKernelGGL((gemm_kernel<kEpiStore, TB>), grid, block, 0, s, a); break;
+    case kEpiResid: hipLaunchKernelGGL((gemm_kernel<kEpiResid, TB>), grid, block, 0, s, a); break;
+    case kEpiQkv: hipLaunchKernelGGL((gemm_kernel<kEpiQkv, TB>), grid, block, 0, s, a); break;
+    case kEpiSwiglu: hipLaunchKernelGGL((gemm_kernel<kEpiSwiglu, TB>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const float *x, const float *g, float eps, float *out, int t, int n, hipStream_t s) {
+    if (t <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)t), dim3(256), 0, s, x, g, eps, out, n);
+    return hipGetLastError();
 }
 
 hipError_t launch_embed(const float *embed, const uint32_t *tokens, float *x, int t, int hidden, hipStream_t s) {

@@ -68,7 +68,7 @@ struct wick_hip_model {
     std::vector<void *> allocs;
     // activations, sized for `cap_t` tokens
     int cap_t = 0;
-    float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *h = nullptr;
+    float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *h = nullptr;
     int cap_logits = 0;  // rows of logits
     float *logits = nullptr;
     int cap_ids = 0;
@@ -88,10 +88,10 @@ int upload(wick_hip_model *m, float **dst, const float *src, size_t n, const cha
 }
 
 void free_activations(wick_hip_model *m) {
-    void *bufs[] = {m->x, m->q, m->k, m->v, m->att, m->h};
+    void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->att, m->h};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
-    m->x = m->q = m->k = m->v = m->att = m->h = nullptr;
+    m->x = m->xn = m->q = m->k = m->v = m->att = m->h = nullptr;
     m->cap_t = 0;
 }
 
@@ -103,8 +103,9 @@ int ensure_activations(wick_hip_model *m, int t) {
     struct {
         float **p;
         size_t n;
-    } want[] = {{&m->x, (size_t)c.hidden}, {&m->q, (size_t)m->qd},  {&m->k, (size_t)m->kvd},
-                {&m->v, (size_t)m->kvd},   {&m->att, (size_t)m->qd}, {&m->h, (size_t)c.intermediate}};
+    } want[] = {{&m->x, (size_t)c.hidden},  {&m->xn, (size_t)c.hidden}, {&m->q, (size_t)m->qd},
+                {&m->k, (size_t)m->kvd},    {&m->v, (size_t)m->kvd},    {&m->att, (size_t)m->qd},
+                {&m->h, (size_t)c.intermediate}};
     for (auto &w : want) {
         hipError_t e = hipMalloc(w.p, (size_t)t * w.n * sizeof(float));
         if (e != hipSuccess) {
@@ -153,6 +154,30 @@ int check_cache(const wick_hip_model *m, const wick_hip_kv *kv, int start, int t
     return WICK_HIP_OK;
 }
 
+// Prompt chunks of at least this many tokens run their products on the matrix
+// cores (gemm_kernel, after a separate RMSNorm pass); shorter ones stream the
+// weights through gemv_kernel, 4 tokens per pass.
+constexpr int kGemmMinTokens = 16;
+
+// One product with a fused epilogue.  g.norm (optional) is the RMSNorm applied
+// to each input row: fused into the GEMV, or a separate pass into m->xn first.
+int product(wick_hip_model *m, int epi, wick::GemvArgs g, const char *what) {
+    hipError_t e;
+    if (g.t >= kGemmMinTokens && g.cols % 16 == 0) {
+        if (g.norm) {
+            if ((e = wick::launch_rmsnorm(g.x, g.norm, g.eps, m->xn, g.t, g.cols, m->stream)) != hipSuccess)
+                return hip_fail(e, "rmsnorm launch");
+            g.x = m->xn;
+            g.norm = nullptr;
+        }
+        e = wick::launch_gemm(epi, g, m->stream);
+    } else {
+        e = wick::launch_gemv(epi, g, m->stream);
+    }
+    if (e != hipSuccess) return hip_fail(e, what);
+    return WICK_HIP_OK;
+}
+
 // Model::forward for t tokens whose ids are on the device; logits of the last
 // token (or of all t when all_logits) go to m->logits.  Queued on m->stream.
 int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, int t, int start, bool all_logits) {
@@ -179,7 +204,7 @@ int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, 
         g.rows = m->qd + 2 * m->kvd;
         g.cols = c.hidden;
         g.t = t;
-        if ((e = wick::launch_gemv(wick::kEpiQkv, g, s)) != hipSuccess) return hip_fail(e, "qkv gemv launch");
+        RC_TRY(product(m, wick::kEpiQkv, g, "qkv product launch"));
 
         RC_TRY(wick::attend_model(kv, li, c.heads, m->q, m->k, m->v, t, start, m->att));
 
@@ -191,7 +216,7 @@ int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, 
         g.rows = c.hidden;
         g.cols = m->qd;
         g.t = t;
-        if ((e = wick::launch_gemv(wick::kEpiResid, g, s)) != hipSuccess) return hip_fail(e, "o gemv launch");
+        RC_TRY(product(m, wick::kEpiResid, g, "o product launch"));
 
         g = wick::GemvArgs{};
         g.x = m->x;
@@ -204,7 +229,7 @@ int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, 
         g.rows = c.intermediate;
         g.cols = c.hidden;
         g.t = t;
-        if ((e = wick::launch_gemv(wick::kEpiSwiglu, g, s)) != hipSuccess) return hip_fail(e, "gate/up gemv launch");
+        RC_TRY(product(m, wick::kEpiSwiglu, g, "gate/up product launch"));
 
         g = wick::GemvArgs{};
         g.x = m->h;
@@ -214,7 +239,7 @@ int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, 
         g.rows = c.hidden;
         g.cols = c.intermediate;
         g.t = t;
-        if ((e = wick::launch_gemv(wick::kEpiResid, g, s)) != hipSuccess) return hip_fail(e, "down gemv launch");
+        RC_TRY(product(m, wick::kEpiResid, g, "down product launch"));
     }
     wick::GemvArgs g{};
     g.x = all_logits ? m->x : m->x + (size_t)(t - 1) * c.hidden;
@@ -226,7 +251,7 @@ int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, 
     g.rows = c.vocab;
     g.cols = c.hidden;
     g.t = all_logits ? t : 1;
-    if ((e = wick::launch_gemv(wick::kEpiStore, g, s)) != hipSuccess) return hip_fail(e, "lm head gemv launch");
+    RC_TRY(product(m, wick::kEpiStore, g, "lm head product launch"));
     return WICK_HIP_OK;
 }
 

@@ -32,6 +32,13 @@ struct GemvArgs {
 // epilogue `epi`; t tokens, cols % 4 == 0.
 hipError_t launch_gemv(int epi, const GemvArgs &a, hipStream_t s);
 
+// The same products for prompt chunks on the matrix cores: a.x holds normalised
+// rows (a.norm must be null), cols % 16 == 0.
+hipError_t launch_gemm(int epi, const GemvArgs &a, hipStream_t s);
+
+// out[i][:] = rmsnorm(x[i][:], g, eps) for i < t rows of n floats.
+hipError_t launch_rmsnorm(const float *x, const float *g, float eps, float *out, int t, int n, hipStream_t s);
+
 // x[i][:] = embed[tokens[i]][:] for i < t (token ids already validated).
 hipError_t launch_embed(const float *embed, const uint32_t *tokens, float *x, int t, int hidden, hipStream_t s);
 
