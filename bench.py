@@ -421,6 +421,11 @@ def main():
                                          f"({step_s * 1e3:.1f} ms/step; {c['heads']} (token, head) items per layer "
                                          f"over a {threads}-thread pool)",
                                "ms_per_step": round(step_s * 1e3, 2)}
+        if threads != 8:
+            # wick's default pool clamps at 8 threads (src/engine.rs:53-56)
+            step8, reps8 = cpu_baseline_decode(kv, q.cpu().numpy(), 8)
+            out["cpu_baseline"]["threads_8"] = {"value": round(bytes_step / step8 / 1e9, 2), "unit": "GB/s",
+                                                "ms_per_step": round(step8 * 1e3, 2), "reps": reps8}
     kv.close()
     print(json.dumps(out), flush=True)
 
