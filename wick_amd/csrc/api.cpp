@@ -58,7 +58,7 @@ struct wick_hip_kv {
     int ws_units = 0;
     // options
     int decode_chunk = 0, pairing = -1, prefill_split = 1, last_grid = 0;
-    int decode_blocks_per_cu = 1;
+    int decode_blocks_per_cu = 1, prefill_blocks_per_cu = 1;
     // input preparation (wick_hip_kv_set_rope / wick_hip_kv_set_prep)
     float *rope_cos = nullptr, *rope_sin = nullptr;  // [capacity][head_dim/2]
     struct LayerPrep {
@@ -200,6 +200,7 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
     a.paired = paired;
     a.items = paired ? (a.nblocks + 1) / 2 : a.nblocks;
     a.split = kv->prefill_split;
+    a.zigzag = (long long)a.kv_heads * a.nblocks <= (long long)kv->num_cus * kv->prefill_blocks_per_cu ? 1 : 0;
     a.scale = scale;
     kv->last_grid = wick::prefill_grid(a);
     hipError_t e = wick::launch_prefill(D, a, kv->stream);
@@ -356,6 +357,7 @@ int wick_hip_kv_create(int layers, int capacity, int kv_heads, int head_dim, wic
         kv->num_cus = prop.multiProcessorCount;
         kv->prep.resize(layers);
         kv->decode_blocks_per_cu = wick::decode_blocks_per_cu(head_dim);
+        kv->prefill_blocks_per_cu = wick::prefill_blocks_per_cu(head_dim);
         if ((e = hipStreamCreateWithFlags(&kv->own_stream, hipStreamNonBlocking)) != hipSuccess) { rc = hip_fail(e, "hipStreamCreate"); break; }
         kv->stream = kv->own_stream;
         const size_t bytes = (size_t)layers * kv->layer_floats() * sizeof(float);

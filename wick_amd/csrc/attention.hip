@@ -597,7 +597,12 @@ __device__ __forceinline__ void prefill_split_body(const PrefillArgs &a) {
     __shared__ float sm_o[4][16][D];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int kvh = blockIdx.x % a.kv_heads;
-    const int b = a.nblocks - 1 - (int)(blockIdx.x / a.kv_heads);
+    // Heaviest causal blocks first.  When the whole grid is resident at once
+    // (zigzag), the second half runs lightest first instead, so that the
+    // workgroups dispatched side by side, idx and idx + nblocks/2, pair a heavy
+    // block with a light one and every CU gets about the same number of tiles.
+    const int idx = (int)(blockIdx.x / a.kv_heads), half = (a.nblocks + 1) >> 1;
+    const int b = (a.zigzag && idx >= half) ? idx - half : a.nblocks - 1 - idx;
     const float *Kh = a.k + (size_t)kvh * a.capacity * D;
     const float *Vh = a.v + (size_t)kvh * a.capacity * D;
     const int col = lane & 15, g = lane >> 4;
@@ -725,6 +730,19 @@ hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_
     const int slices = head_dim / 16;
     WICK_DISPATCH_D(head_dim, decode_merge_kernel, dim3(units * 16 * slices), dim3(256), 0, s, a);
     return hipGetLastError();
+}
+
+int prefill_blocks_per_cu(int head_dim) {
+    int n = 0;
+    hipError_t e = hipErrorInvalidValue;
+    switch (head_dim) {
+    case 16: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_split_kernel<16>, 256, 0); break;
+    case 32: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_split_kernel<32>, 256, 0); break;
+    case 64: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_split_kernel<64>, 256, 0); break;
+    case 128: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_split_kernel_d128, 256, 0); break;
+    default: break;
+    }
+    return (e == hipSuccess && n > 0) ? n : 1;
 }
 
 int prefill_grid(const PrefillArgs &a) {

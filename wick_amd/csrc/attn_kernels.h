@@ -40,6 +40,7 @@ struct PrefillArgs {
     float *att;       // [t][heads*D]
     int capacity, t, start, kv_heads, group, nblocks, items, paired;
     int split;        // 1: prefill_split_kernel (4-way key split per workgroup)
+    int zigzag;       // split kernel: the grid is resident at once; pair heavy and light blocks
     float scale;
 };
 
@@ -65,6 +66,8 @@ size_t decode_workspace_floats(int units, int head_dim);
 
 // Decode workgroups one CU holds at once (from the kernel's register and LDS use).
 int decode_blocks_per_cu(int head_dim);
+// The same for the split prefill kernel.
+int prefill_blocks_per_cu(int head_dim);
 
 // Launches decode_kernel and, when it splits the keys, decode_merge_kernel.
 hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_t s);
