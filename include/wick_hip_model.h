@@ -12,7 +12,9 @@
  *     per-token preparation + Model::attention of wick_hip.h;
  *   - sampler::argmax (/root/reference/src/sampler.rs:129-137) and the greedy
  *     loop of cmd_bench (/root/reference/src/main.rs:223-258) with its 256-token
- *     prefill chunks (Session::prefill, /root/reference/src/engine.rs:107, :134).
+ *     prefill chunks (Session::prefill, /root/reference/src/engine.rs:107, :134);
+ *   - the token loop of Session::generate (/root/reference/src/engine.rs:164-204)
+ *     with the sampler of wick_hip_sampler.h.
  *
  * Conventions are those of wick_hip.h: int status codes (WICK_HIP_OK or a
  * negative WICK_HIP_E*), wick_hip_last_error() for the message, borrowed host
@@ -27,6 +29,7 @@
 #include <stdint.h>
 
 #include "wick_hip.h"
+#include "wick_hip_sampler.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -77,6 +80,29 @@ int wick_hip_model_prefill(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *p
  * out[i] and the input of forward i+1.  Ids stay on the device between
  * steps; the call returns when out [steps] (host) is filled. */
 int wick_hip_model_decode(wick_hip_model *m, wick_hip_kv *kv, uint32_t first, int start, int steps, uint32_t *out);
+
+/* Sampler::new (src/sampler.rs:67-71) for this model's vocabulary, launching
+ * on the model's stream (wick_hip_sampler.h).  Destroy it with
+ * wick_hip_sampler_destroy. */
+int wick_hip_model_new_sampler(wick_hip_model *m, const wick_hip_sampler_config *cfg, wick_hip_sampler **out);
+
+/* The token loop of Session::generate (/root/reference/src/engine.rs:164-204)
+ * on the device; detokenising and stop strings stay with the caller.
+ *   tokens [n] (host) is the session's whole token list; the cache already
+ *   holds the first `start` of them (0 <= start < n), and tokens[start..n) run
+ *   in chunks of 256 (Session::prefill, :120-139).
+ *   Up to max_tokens ids are then drawn with the sampler, clamped to the room
+ *   left in the cache (:167-169); every drawn id but the last is fed back
+ *   (:200-202).  The repetition penalty reads tokens plus the ids drawn so
+ *   far (self.tokens, :179).
+ *   An id listed in stops [n_stops] ends the loop; it is neither output nor
+ *   fed (:181-184).  With stops the host reads each id while the next step
+ *   runs, so one step past a stop is computed and discarded.
+ * out [max_tokens] (host) receives *n_out ids; *cache_len receives the number
+ * of positions the cache holds afterwards (n plus the ids fed). */
+int wick_hip_model_generate(wick_hip_model *m, wick_hip_kv *kv, wick_hip_sampler *s, const uint32_t *tokens, int n,
+                            int start, int max_tokens, const uint32_t *stops, int n_stops, uint32_t *out, int *n_out,
+                            int *cache_len);
 
 #ifdef __cplusplus
 }

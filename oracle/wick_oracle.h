@@ -84,6 +84,30 @@ int wo_forward(const wo_model *m, float *cache_k, float *cache_v, int capacity, 
 /* sampler::argmax (src/sampler.rs:129-137): first index of the maximum. */
 uint32_t wo_argmax(const float *x, int n);
 
+/* ---- the sampler (/root/reference/src/sampler.rs), oracle/wick_sampler.c ---- */
+
+/* SamplerConfig (src/sampler.rs:3-14). */
+typedef struct {
+    float temperature;
+    uint32_t top_k;
+    float top_p;
+    float min_p;
+    float repetition_penalty;
+    uint64_t seed;
+} wo_sampler_config;
+
+/* Rng::new, next_u64, next_f32 (src/sampler.rs:33-60). */
+void wo_rng_seed(uint64_t seed, uint64_t s[4]);
+uint64_t wo_rng_next_u64(uint64_t s[4]);
+float wo_rng_next_f32(uint64_t s[4]);
+
+/* Sampler::sample (src/sampler.rs:73-127) with generator state rng[4]:
+ * logits [n] are penalised in place; returns the drawn id.  Optionally the k
+ * sorted candidates (ids_out, probs_out after normalisation, capacity n) and
+ * the kept count; *k_out = *keep_out = 0 after a greedy draw. */
+uint32_t wo_sample(const wo_sampler_config *cfg, uint64_t rng[4], float *logits, int n, const uint32_t *history,
+                   int n_history, uint32_t *ids_out, float *probs_out, int *k_out, int *keep_out);
+
 #ifdef __cplusplus
 }
 #endif

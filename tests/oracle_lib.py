@@ -27,6 +27,11 @@ class WoModel(ctypes.Structure):
                 ("lm_head", _FP), ("norm", _FP), ("layer", ctypes.POINTER(WoLayer))]
 
 
+class WoSamplerConfig(ctypes.Structure):
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_uint32), ("top_p", ctypes.c_float),
+                ("min_p", ctypes.c_float), ("repetition_penalty", ctypes.c_float), ("seed", ctypes.c_uint64)]
+
+
 def load():
     global _lib
     if _lib is None:
@@ -48,6 +53,14 @@ def load():
         lib.wo_forward.argtypes = [ctypes.POINTER(WoModel), P, P, I, ctypes.POINTER(I), P, I, I, P, I, I, P, P]
         lib.wo_argmax.restype = ctypes.c_uint32
         lib.wo_argmax.argtypes = [P, I]
+        lib.wo_rng_seed.argtypes = [ctypes.c_uint64, P]
+        lib.wo_rng_next_u64.restype = ctypes.c_uint64
+        lib.wo_rng_next_u64.argtypes = [P]
+        lib.wo_rng_next_f32.restype = ctypes.c_float
+        lib.wo_rng_next_f32.argtypes = [P]
+        lib.wo_sample.restype = ctypes.c_uint32
+        lib.wo_sample.argtypes = [ctypes.POINTER(WoSamplerConfig), P, P, I, P, I, P, P, ctypes.POINTER(I),
+                                  ctypes.POINTER(I)]
         _lib = lib
     return _lib
 
@@ -190,3 +203,50 @@ class OracleModel:
         if trace:
             return logits, qt, at
         return logits
+
+
+class OracleRng:
+    """Rng (src/sampler.rs:29-60) restated."""
+
+    def __init__(self, seed=None, state=None):
+        self.s = (ctypes.c_uint64 * 4)()
+        if state is not None:
+            for i in range(4):
+                self.s[i] = state[i]
+        else:
+            load().wo_rng_seed(seed, self.s)
+
+    def state(self):
+        return tuple(int(v) for v in self.s)
+
+    def next_u64(self):
+        return int(load().wo_rng_next_u64(self.s))
+
+    def next_f32(self):
+        return float(load().wo_rng_next_f32(self.s))
+
+
+class OracleSampler:
+    """Sampler::new + Sampler::sample (src/sampler.rs:62-127) restated; cfg is any
+    object with SamplerConfig's fields."""
+
+    def __init__(self, cfg):
+        self.cfg = WoSamplerConfig(cfg.temperature, cfg.top_k, cfg.top_p, cfg.min_p, cfg.repetition_penalty,
+                                   cfg.seed)
+        self.rng = OracleRng(cfg.seed)
+
+    def sample(self, logits, history=()):
+        """logits: float32 array, penalised in place as wick's &mut [f32]."""
+        return self.sample_detail(logits, history)[0]
+
+    def sample_detail(self, logits, history=()):
+        """(id, candidate ids [k], their probabilities [k], keep)."""
+        assert logits.dtype == np.float32 and logits.flags.c_contiguous
+        n = logits.size
+        hist = _c(history, np.uint32)
+        ids = np.empty(n, np.uint32)
+        probs = np.empty(n, np.float32)
+        k, keep = ctypes.c_int(), ctypes.c_int()
+        tok = load().wo_sample(ctypes.byref(self.cfg), self.rng.s, _p(logits), n, _p(hist), hist.size, _p(ids),
+                               _p(probs), ctypes.byref(k), ctypes.byref(keep))
+        return int(tok), ids[:k.value].copy(), probs[:k.value].copy(), keep.value

@@ -58,6 +58,21 @@ def test_argument_errors_without_device_work():
     assert lib.wick_hip_model_forward(None, None, None, 1, 0, 0, None) == _native.EINVAL
     assert lib.wick_hip_model_prefill(None, None, None, 1, 0, None) == _native.EINVAL
     assert lib.wick_hip_model_decode(None, None, 0, 0, 1, None) == _native.EINVAL
+    assert lib.wick_hip_model_new_sampler(None, None, ctypes.byref(m)) == _native.EINVAL
+    n = ctypes.c_int()
+    assert lib.wick_hip_model_generate(None, None, None, None, 1, 0, 1, None, 0, None, ctypes.byref(n),
+                                       ctypes.byref(n)) == _native.EINVAL
+    from wick_amd.sampler import SamplerConfig, c_config
+    cfg = c_config(SamplerConfig())
+    assert lib.wick_hip_sampler_create(None, 10, None, ctypes.byref(m)) == _native.EINVAL
+    assert lib.wick_hip_sampler_create(ctypes.byref(cfg), 0, None, ctypes.byref(m)) == _native.EINVAL
+    assert b"vocab" in lib.wick_hip_last_error()
+    assert lib.wick_hip_sampler_create(ctypes.byref(cfg), 10, None, None) == _native.EINVAL
+    lib.wick_hip_sampler_destroy(None)
+    assert lib.wick_hip_sampler_sample(None, None, None, 0, None) == _native.EINVAL
+    assert lib.wick_hip_sampler_sample_device(None, None, None, 0, None) == _native.EINVAL
+    assert lib.wick_hip_sampler_rng_state(None, None) == _native.EINVAL
+    assert lib.wick_hip_sampler_last_candidates(None, None, None, None, None, 0) == _native.EINVAL
 
 
 def test_no_device_is_an_error_not_a_fallback():
@@ -71,6 +86,10 @@ def test_no_device_is_an_error_not_a_fallback():
     h = ctypes.c_void_p()
     rc = lib.wick_hip_kv_create(1, 16, 2, 64, ctypes.byref(h))
     assert rc == _native.EDEVICE, rc
+    assert not h.value
+    from wick_amd.sampler import SamplerConfig, c_config
+    cfg = c_config(SamplerConfig())
+    assert lib.wick_hip_sampler_create(ctypes.byref(cfg), 100, None, ctypes.byref(h)) == _native.EDEVICE
     assert not h.value
 
 

@@ -1,4 +1,4 @@
-"""ctypes bindings of the C ABI in include/wick_hip.h and include/wick_hip_model.h.
+"""ctypes bindings of the C ABI in include/wick_hip.h, wick_hip_model.h and wick_hip_sampler.h.
 
 This is the binding a host program writes for the library (the Rust side would
 declare the same symbols in an `extern "C"` block).  There is no fallback: if
@@ -48,6 +48,15 @@ SIGNATURES = {
     "wick_hip_model_forward": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "wick_hip_model_prefill": (_I, [_P, _P, _P, _I, _I, _P]),
     "wick_hip_model_decode": (_I, [_P, _P, ctypes.c_uint32, _I, _I, _P]),
+    "wick_hip_model_new_sampler": (_I, [_P, _P, ctypes.POINTER(_P)]),
+    "wick_hip_model_generate": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _I, _P, _P, _P]),
+    # wick_hip_sampler.h
+    "wick_hip_sampler_create": (_I, [_P, _I, _P, ctypes.POINTER(_P)]),
+    "wick_hip_sampler_destroy": (None, [_P]),
+    "wick_hip_sampler_sample_device": (_I, [_P, _P, _P, _I, _P]),
+    "wick_hip_sampler_sample": (_I, [_P, _P, _P, _I, _P]),
+    "wick_hip_sampler_rng_state": (_I, [_P, _P]),
+    "wick_hip_sampler_last_candidates": (_I, [_P, _P, _P, _P, _P, _I]),
 }
 
 _lib = None

@@ -31,7 +31,8 @@ def _run(cmd):
 
 def build_hip():
     out = os.path.join(HERE, "libwick_hip.so")
-    srcs = [os.path.join(CSRC, f) for f in ("attention.hip", "prep.hip", "model.hip", "api.cpp", "model_api.cpp")]
+    srcs = [os.path.join(CSRC, f) for f in ("attention.hip", "prep.hip", "model.hip", "sampler.hip", "api.cpp", "model_api.cpp",
+                                             "sampler_api.cpp")]
     _run([HIPCC, *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", out + ".tmp"])
     os.replace(out + ".tmp", out)
     return out

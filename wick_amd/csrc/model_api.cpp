@@ -21,6 +21,7 @@
 
 #include "attn_kernels.h"
 #include "model_kernels.h"
+#include "sampler_kernels.h"
 
 namespace {
 
@@ -73,6 +74,7 @@ struct wick_hip_model {
     float *logits = nullptr;
     int cap_ids = 0;
     uint32_t *ids = nullptr;  // token ids on the device (prompt, or the greedy chain)
+    uint32_t *pinned_id = nullptr;  // page-locked slot the generate loop reads ids through
 };
 
 namespace {
@@ -369,6 +371,7 @@ void wick_hip_model_destroy(wick_hip_model *m) {
     free_activations(m);
     if (m->logits) (void)hipFree(m->logits);
     if (m->ids) (void)hipFree(m->ids);
+    if (m->pinned_id) (void)hipHostFree(m->pinned_id);
     for (void *p : m->allocs) (void)hipFree(p);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
@@ -442,6 +445,87 @@ int wick_hip_model_decode(wick_hip_model *m, wick_hip_kv *kv, uint32_t first, in
     HIP_TRY(hipMemcpyAsync(out, m->ids + 1, (size_t)steps * sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream));
     HIP_TRY(hipStreamSynchronize(m->stream));
     return WICK_HIP_OK;
+}
+
+int wick_hip_model_new_sampler(wick_hip_model *m, const wick_hip_sampler_config *cfg, wick_hip_sampler **out) {
+    if (!m) return set_error(WICK_HIP_EINVAL, "null argument");
+    return wick_hip_sampler_create(cfg, m->c.vocab, m->stream, out);
+}
+
+int wick_hip_model_generate(wick_hip_model *m, wick_hip_kv *kv, wick_hip_sampler *s, const uint32_t *tokens, int n,
+                            int start, int max_tokens, const uint32_t *stops, int n_stops, uint32_t *out, int *n_out,
+                            int *cache_len) {
+    if (!m || !s || !tokens || !n_out || !cache_len || (max_tokens > 0 && !out))
+        return set_error(WICK_HIP_EINVAL, "null argument");
+    if (max_tokens < 0) return set_error(WICK_HIP_EINVAL, "max_tokens must be >= 0 (got %d)", max_tokens);
+    if (n_stops < 0 || (n_stops > 0 && !stops)) return set_error(WICK_HIP_EINVAL, "bad stop list");
+    if (wick::sampler_stream(s) != m->stream)
+        return set_error(WICK_HIP_EINVAL, "sampler launches on another stream (make it with wick_hip_model_new_sampler)");
+    if (wick::sampler_vocab(s) != m->c.vocab)
+        return set_error(WICK_HIP_EINVAL, "sampler vocabulary %d != model vocabulary %d", wick::sampler_vocab(s),
+                         m->c.vocab);
+    if (start < 0 || start >= n)
+        return set_error(WICK_HIP_EINVAL, "start %d must be in [0, n = %d): the last token is run for its logits",
+                         start, n);
+    RC_TRY(check_cache(m, kv, start, n - start));
+    RC_TRY(check_tokens(m, tokens, n));
+    wick::KvInfo ki;
+    wick::kv_info(kv, &ki);
+    max_tokens = std::min(max_tokens, ki.capacity - n);  // room (src/engine.rs:167-168)
+    *n_out = 0;
+    *cache_len = n;
+    RC_TRY(ensure_ids(m, n + std::max(max_tokens, 1)));
+    RC_TRY(upload_ids(m, tokens, n));
+    for (int off = start; off < n; off += kPrefillChunk) {
+        const int t = std::min(kPrefillChunk, n - off);
+        RC_TRY(forward_device(m, kv, m->ids + off, t, off, false));
+    }
+    const bool history = wick::sampler_reads_history(s);
+    auto step = [&](int j) -> int {
+        RC_TRY(wick::sampler_enqueue(s, m->logits, m->ids, history ? n + j : 0, m->ids + n + j));
+        if (n_stops > 0) {
+            HIP_TRY(hipMemcpyAsync(m->pinned_id, m->ids + n + j, sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream));
+        }
+        return WICK_HIP_OK;
+    };
+    if (n_stops == 0) {
+        for (int j = 0; j < max_tokens; j++) {
+            RC_TRY(step(j));
+            if (j + 1 < max_tokens) RC_TRY(forward_device(m, kv, m->ids + n + j, 1, n + j, false));
+        }
+        if (max_tokens > 0)
+            HIP_TRY(hipMemcpyAsync(out, m->ids + n, (size_t)max_tokens * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                                   m->stream));
+        HIP_TRY(hipStreamSynchronize(m->stream));
+        *n_out = max_tokens;
+        *cache_len = n + std::max(max_tokens - 1, 0);
+        return WICK_HIP_OK;
+    }
+    if (!m->pinned_id) HIP_TRY(hipHostMalloc((void **)&m->pinned_id, 64, hipHostMallocDefault));
+    hipEvent_t ev = nullptr;
+    HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    int rc = WICK_HIP_OK;
+    for (int j = 0; j < max_tokens && !rc; j++) {
+        if ((rc = step(j))) break;
+        hipError_t e = hipEventRecord(ev, m->stream);
+        // queue the next forward before reading the id, so the GPU keeps working
+        if (e == hipSuccess && j + 1 < max_tokens) rc = forward_device(m, kv, m->ids + n + j, 1, n + j, false);
+        if (e == hipSuccess && !rc) e = hipEventSynchronize(ev);
+        if (e != hipSuccess) {
+            rc = hip_fail(e, "generate: reading the drawn id");
+            break;
+        }
+        if (rc) break;
+        const uint32_t tok = *m->pinned_id;
+        if (std::find(stops, stops + n_stops, tok) != stops + n_stops) break;
+        out[j] = tok;
+        *n_out = j + 1;
+        *cache_len = n + (j + 1 < max_tokens ? j + 1 : j);
+    }
+    hipError_t e = hipStreamSynchronize(m->stream);
+    (void)hipEventDestroy(ev);
+    if (!rc && e != hipSuccess) rc = hip_fail(e, "generate");
+    return rc;
 }
 
 }  // extern "C"

@@ -4,7 +4,9 @@ DeviceModel mirrors wick's Model (/root/reference/src/model.rs:152-249) for f32
 weights; new_cache() is State::new (:300-302); forward() is Model::forward
 (:420-516); prefill() / decode() are Session::prefill (src/engine.rs:120-139)
 and the greedy loop of cmd_bench (src/main.rs:223-258) with sampler::argmax
-(src/sampler.rs:129-137) on the device.
+(src/sampler.rs:129-137) on the device; new_sampler() / generate() are
+Sampler::new (src/sampler.rs:67-71) and the token loop of Session::generate
+(src/engine.rs:164-204) with the sampler on the device.
 """
 import ctypes
 
@@ -13,6 +15,7 @@ import numpy as np
 from . import _native
 from .kv import DeviceKvCache
 from .model import LAYER_TENSORS
+from .sampler import DeviceSampler, c_config
 
 
 class ModelConfig(ctypes.Structure):
@@ -103,3 +106,25 @@ class DeviceModel:
                                                       out.ctypes.data))
         cache.len += steps
         return [int(i) for i in out]
+
+    def new_sampler(self, cfg):
+        """Sampler::new for this model's vocabulary, on the model's stream."""
+        h = ctypes.c_void_p()
+        c = c_config(cfg)
+        _native.check(self._lib.wick_hip_model_new_sampler(self.handle, ctypes.byref(c), ctypes.byref(h)))
+        return DeviceSampler(cfg, self.cfg.vocab, handle=h)
+
+    def generate(self, cache, sampler, tokens, max_tokens, stops=()):
+        """Session::generate's token loop: tokens is the session's whole token list, of
+        which the cache holds the first cache.len; returns the drawn ids (a stop id
+        ends the list and is not included).  cache.len is updated to what the cache
+        holds afterwards."""
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+        st = np.ascontiguousarray(list(stops), dtype=np.uint32).reshape(-1)
+        out = np.empty(max(int(max_tokens), 1), np.uint32)
+        n_out, clen = ctypes.c_int(), ctypes.c_int()
+        _native.check(self._lib.wick_hip_model_generate(self.handle, cache.handle, sampler.handle, toks.ctypes.data,
+                                                        toks.size, cache.len, int(max_tokens), st.ctypes.data, st.size,
+                                                        out.ctypes.data, ctypes.byref(n_out), ctypes.byref(clen)))
+        cache.len = clen.value
+        return [int(i) for i in out[:n_out.value]]
