@@ -257,6 +257,22 @@ def measure_e2e():
         cache.close()
         if rep and (best is None or t2 - t1 < best[1]):
             best = (t1 - t0, t2 - t1, ids)
+    # (3) the same, drawing with wick's default sampler on the device (Session::generate's
+    #     loop): the cache holds the prompt but its last token, generate() runs that token,
+    #     then n_gen + 1 draws and n_gen single-token forwards
+    from wick_amd.sampler import SamplerConfig
+    best_s = None
+    for rep in range(3):
+        cache = dm.new_cache(128 + n_gen + 8)
+        dm.prefill(cache, prompt[:-1])
+        smp = dm.new_sampler(SamplerConfig())
+        t0 = time.perf_counter()
+        dm.generate(cache, smp, prompt, n_gen + 1)
+        t1 = time.perf_counter()
+        smp.close()
+        cache.close()
+        if rep and (best_s is None or t1 - t0 < best_s):
+            best_s = t1 - t0
     dm.close()
     del w
     return {"workload": f"random-init SmolLM2-135M architecture, f32, 128-token prompt + {n_gen} greedy "
@@ -264,8 +280,36 @@ def measure_e2e():
             "device_resident": {"prompt_tok_s": round(128 / best[0], 1),
                                 "decode_tok_s": round(n_gen / best[1], 2),
                                 "ms_per_token": round(best[1] * 1e3 / n_gen, 3)},
+            "device_resident_sampled": {"decode_tok_s": round((n_gen + 1) / best_s, 2),
+                                        "ms_per_token": round(best_s * 1e3 / (n_gen + 1), 3),
+                                        "sampler": "SamplerConfig::default() (temperature 0.7, top-k 40, top-p 0.9)"},
+            "sampler_draw_us": {str(v): time_sampler(v) for v in (cfg.vocab, 151936)},
             "host_forward_gpu_attention": host,
             "greedy_ids_identical": best[2] == host_ids}
+
+
+def time_sampler(vocab, draws=200):
+    """One device draw (SamplerConfig::default()) over an LM-head-like logit vector, by
+    HIP events around `draws` back-to-back launches on the sampler's stream."""
+    import numpy as np
+    import torch
+    from wick_amd.sampler import DeviceSampler, SamplerConfig
+    stream = torch.cuda.current_stream()
+    rng = np.random.default_rng(0)
+    x = rng.normal(-5, 2, vocab)
+    x[rng.integers(0, vocab, max(1, vocab // 1000))] += 12
+    logits = torch.from_numpy(x.astype(np.float32)).cuda()
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    with DeviceSampler(SamplerConfig(), vocab, stream=stream.cuda_stream) as ds:
+        for _ in range(10):
+            ds.sample_device(logits.data_ptr(), None, 0, out.data_ptr())
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(draws):
+            ds.sample_device(logits.data_ptr(), None, 0, out.data_ptr())
+        e1.record(stream)
+        e1.synchronize()
+    return round(e0.elapsed_time(e1) * 1e3 / draws, 2)
 
 
 def main():

@@ -44,6 +44,9 @@ def logits_of(kind, n, rng):
     elif kind == "lm":  # a peaked head over a long tail
         x = rng.normal(-5, 2, n)
         x[rng.integers(0, n, max(1, n // 1000))] += 12
+    elif kind == "const":  # every slice is one run of ties: the split top-k falls back to the full path
+        x = np.full(n, 0.5)
+        x[rng.integers(0, n, 3)] = 1.5
     elif kind == "nan":
         x = rng.normal(0, 3, n)
         x[rng.integers(0, n)] = np.nan
@@ -81,7 +84,7 @@ def check_draw(ds, os_, logits, history, name):
 def test_sampler_matches_oracle(vocab, name):
     cfg = CONFIGS[name]
     rng = np.random.default_rng(vocab + len(name))
-    kinds = ["normal", "flat", "ties", "lm"] + (["nan"] if name in ("default", "whole_vocab") else [])
+    kinds = ["normal", "flat", "ties", "lm"] + (["nan", "const"] if name in ("default", "whole_vocab", "top1") else [])
     draws = 2 if vocab > 50000 else 4
     with DeviceSampler(cfg, vocab) as ds:
         os_ = ol.OracleSampler(cfg)

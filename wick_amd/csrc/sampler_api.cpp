@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -21,6 +22,11 @@ struct wick_hip_sampler {
     uint32_t *key0 = nullptr, *key1 = nullptr, *idx1 = nullptr, *res_idx = nullptr;
     float *res_prob = nullptr;
     int *meta = nullptr;
+    int parts = 1, slice = 32;
+    float *part_val = nullptr;
+    uint32_t *part_id = nullptr;
+    unsigned long long *part_cand = nullptr;
+    int *part_count = nullptr;
     // staging for the host-array entry point
     float *logits = nullptr;
     uint32_t *out = nullptr;
@@ -55,8 +61,8 @@ void seed_rng(uint64_t seed, uint64_t out[4]) {
 }
 
 void release(wick_hip_sampler *s) {
-    void *bufs[] = {s->flags, s->rng, s->key0, s->key1, s->idx1, s->res_idx, s->res_prob, s->meta,
-                    s->logits, s->out, s->history};
+    void *bufs[] = {s->flags, s->rng,      s->key0,     s->key1,      s->idx1,       s->res_idx, s->res_prob, s->meta,
+                    s->part_val, s->part_id, s->part_cand, s->part_count, s->logits, s->out,     s->history};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
 }
@@ -96,6 +102,13 @@ int sampler_enqueue(wick_hip_sampler *s, float *logits, const uint32_t *history,
     a.res_idx = s->res_idx;
     a.res_prob = s->res_prob;
     a.res_meta = s->meta;
+    a.parts = s->parts;
+    a.slice = s->slice;
+    a.split_top_k = s->slice <= kSliceMax;
+    a.part_val = s->part_val;
+    a.part_id = s->part_id;
+    a.part_cand = s->part_cand;
+    a.part_count = s->part_count;
     hipError_t e = launch_sample(a, s->stream);
     if (e != hipSuccess) return hip_fail(e, "sample launch");
     return WICK_HIP_OK;
@@ -120,14 +133,20 @@ int wick_hip_sampler_create(const wick_hip_sampler_config *cfg, int vocab, void 
     s->cfg = *cfg;
     s->vocab = vocab;
     s->stream = static_cast<hipStream_t>(stream);
-    const size_t n = (size_t)vocab, words = (n + 31) / 32;
+    // slices of the split kernel: whole bitset words, about 4096 ids or more each
+    s->parts = std::min(wick::kSampleParts, (vocab + 4095) / 4096);
+    s->slice = ((vocab + s->parts - 1) / s->parts + 31) / 32 * 32;
+    s->parts = (vocab + s->slice - 1) / s->slice;
+    const size_t n = (size_t)vocab, words = (n + 31) / 32, np = wick::kSampleParts;
     struct {
         void **p;
         size_t bytes;
     } want[] = {{(void **)&s->flags, words * 4},   {(void **)&s->rng, 32},        {(void **)&s->key0, n * 4},
                 {(void **)&s->key1, n * 4},        {(void **)&s->idx1, n * 4},    {(void **)&s->res_idx, n * 4},
                 {(void **)&s->res_prob, n * 4},    {(void **)&s->meta, 16},       {(void **)&s->logits, n * 4},
-                {(void **)&s->out, 16}};
+                {(void **)&s->out, 16},            {(void **)&s->part_val, np * 4},
+                {(void **)&s->part_id, np * 4},    {(void **)&s->part_cand, np * wick::kFastK * 8},
+                {(void **)&s->part_count, np * 4}};
     int rc = WICK_HIP_OK;
     for (auto &w : want) {
         hipError_t e = hipMalloc(w.p, w.bytes);

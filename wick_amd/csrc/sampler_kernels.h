@@ -8,6 +8,10 @@ struct wick_hip_sampler;
 
 namespace wick {
 
+constexpr int kSampleParts = 16;  // most workgroups of the split kernel
+constexpr int kFastK = 64;        // top-k up to this is taken per slice, then merged
+constexpr int kSliceMax = 12288;  // longest slice whose keys the split kernel holds in registers
+
 // One draw of Sampler::sample (/root/reference/src/sampler.rs:73-127).
 struct SampleArgs {
     float *logits;  // [vocab], 16-byte aligned; penalised in place
@@ -25,6 +29,16 @@ struct SampleArgs {
     uint32_t *res_idx;  // [vocab] the candidates in wick's order
     float *res_prob;    // [vocab] their probabilities after normalisation
     int *res_meta;      // {k, keep, internal check (0 = ok)}
+    // The split kernel: `parts` slices of `slice` ids (a multiple of 32), each
+    // leaving its argmax in part_val/part_id or its k best (key << 32 | id) in
+    // part_cand[g * kFastK ..] with their count in part_count[g] (-1: too many
+    // ties, the final kernel takes the whole vocabulary).
+    int parts, slice;
+    int split_top_k;  // slices fit kSliceMax
+    float *part_val;
+    uint32_t *part_id;
+    unsigned long long *part_cand;
+    int *part_count;
 };
 
 hipError_t launch_sample(const SampleArgs &a, hipStream_t s);
