@@ -40,7 +40,6 @@ constexpr int kMaxBins = 2048;         // 11-bit digits
 constexpr int kList = 4096;            // largest candidate set sorted in LDS
 constexpr int kSlicePer = kSliceMax / kT;  // slice entries per thread in the split kernel
 constexpr int kPartCand = 1024;        // candidates one slice may hold at its k-th key
-constexpr int kSplitSort = 256;        // the split select refines until at most this many remain
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
@@ -517,7 +516,7 @@ __global__ __launch_bounds__(kT) void sample_split_kernel(SampleArgs a) {
                 for (int j = 0; j < kSlicePer; j++)
                     if (lo + j * kT + tid < hi) f(key[j]);
             },
-            k, (uint32_t)kSplitSort, s, &bound);
+            k, 64u, s, &bound);
     if (tid == 0) s.count = 0u;
     __syncthreads();
     if (nset > (uint32_t)kPartCand) {  // too many ties: the final kernel takes the whole vocabulary
@@ -534,7 +533,12 @@ __global__ __launch_bounds__(kT) void sample_split_kernel(SampleArgs a) {
     }
     __syncthreads();
     const int n = (int)min(s.count, (uint32_t)kPartCand);
-    if (tid < n) {
+    if (n <= 64) {  // one wave sorts them
+        if (tid < 64) {
+            const unsigned long long c = wave_sort(tid < n ? s.l.cand[tid] : ~0ull);
+            if (tid < min(n, (int)k)) a.part_cand[g * kFastK + tid] = c;
+        }
+    } else if (tid < n) {
         const unsigned long long c = s.l.cand[tid];
         const int r = rank_of(c, s.l.cand, n);
         if (r < (int)k) a.part_cand[g * kFastK + r] = c;
