@@ -373,7 +373,11 @@ struct DecodeSpace {
 // written directly; otherwise the chunk's (max, sum, O) state per query head
 // goes to the workspace and decode_merge_kernel, the next launch on the
 // stream, combines them (the kernel boundary orders the two).
-template <int D, bool PREP>
+// PP: double-buffer the tile loads of consecutive groups.  When every wave
+// takes at most one group (short chunks) the second buffer only costs
+// registers -- 184 against 87 VGPRs at head_dim 64 -- so the launcher picks
+// the single-buffered instance then.
+template <int D, bool PREP, bool PP = (D < 128)>
 __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     using S = Shape<D>;
     __shared__ float sm_m[4][16], sm_l[4][16];
@@ -423,7 +427,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 
     WaveState<D> st;
     init_state<D>(st);
-    attend_range<D, (D < 128)>(Kh, Vh, kbeg, kend, w * S::TG, 4 * S::TG, a.len, a.scale, q, lane, st);
+    attend_range<D, PP>(Kh, Vh, kbeg, kend, w * S::TG, 4 * S::TG, a.len, a.scale, q, lane, st);
     st.l = col_sum(st.l);
 
     if (g == 0) {
@@ -464,8 +468,9 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     }
 }
 
-// Merge pass: workgroup (unit, column, 16-dim slice) combines the nchunks
-// (<= 256) partial states of one query head for 16 of its head dims.  Thread
+// Merge pass: workgroup (query head, 16-dim slice) combines the nchunks
+// (<= 256) partial states of one query head for 16 of its head dims; the grid
+// holds exactly heads x D/16 workgroups.  Thread
 // (grp, dd) of 16 groups owns children grp, grp + 16, ...: it loads their O, m
 // and l together (one memory round trip), merges them by log-sum-exp against
 // its own running max, and a single LDS step combines the 16 group states the
@@ -479,10 +484,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
     constexpr int NB = kDecodeMaxChunks / G;      // children per thread
     __shared__ float sm[G][DW], so[G][DW], sl[G][DW];
     const int units = a.kv_heads * a.hslices;
-    const int ds = blockIdx.x % NS, col = (blockIdx.x / NS) % 16, unit = blockIdx.x / (NS * 16);
-    const int kvh = unit / a.hslices, slice = unit % a.hslices;
-    const int col0 = slice * 16, ncols = min(16, a.group - col0);
-    if (col >= ncols) return;
+    const int ds = blockIdx.x % NS, head = blockIdx.x / NS;
+    const int kvh = head / a.group, hh = head % a.group;
+    const int col = hh % 16, unit = kvh * a.hslices + hh / 16;
     const DecodeSpace<D> ws(a.part, units);
     const size_t base = DecodeSpace<D>::at(unit, col, 0);
     const float *o = ws.o + base * D + ds * DW, *m = ws.m + base, *l = ws.l + base;
@@ -525,7 +529,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
             ot += so[gg][tid] * e;
             Lt += sl[gg][tid] * e;
         }
-        a.att[(size_t)(kvh * a.group + col0 + col) * D + ds * DW + tid] = ot / Lt;
+        a.att[(size_t)head * D + ds * DW + tid] = ot / Lt;
     }
 }
 
@@ -710,6 +714,17 @@ int decode_blocks_per_cu(int head_dim) {
 
 template <int D>
 void launch_decode_d(const DecodeArgs &a, int grid, hipStream_t s) {
+    // each of the 4 waves takes groups of TG 16-key tiles, stepping by 4 groups
+    const bool one_group = a.chunk <= 4 * Shape<D>::TG * 16;
+    if constexpr (D < 128) {
+        if (one_group) {
+            if (a.prep)
+                hipLaunchKernelGGL((decode_kernel<D, true, false>), dim3(grid), dim3(256), 0, s, a);
+            else
+                hipLaunchKernelGGL((decode_kernel<D, false, false>), dim3(grid), dim3(256), 0, s, a);
+            return;
+        }
+    }
     if (a.prep)
         hipLaunchKernelGGL((decode_kernel<D, true>), dim3(grid), dim3(256), 0, s, a);
     else
@@ -726,9 +741,8 @@ hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nchunks == 1) return e;
-    const int units = a.kv_heads * a.hslices;
     const int slices = head_dim / 16;
-    WICK_DISPATCH_D(head_dim, decode_merge_kernel, dim3(units * 16 * slices), dim3(256), 0, s, a);
+    WICK_DISPATCH_D(head_dim, decode_merge_kernel, dim3(a.kv_heads * a.group * slices), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
