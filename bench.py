@@ -206,11 +206,26 @@ def measure_long_decode(torch, kv_cls, native, dev, steps):
                       "us_per_layer": round(ms_launch * 1e3, 2), "GBps": round(gbs, 1),
                       "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 1)})
     kv.set_option(native.OPT_DECODE_CHUNK, 0)
+
+    # The same shape at a 32K context (the first 32768 positions of each layer,
+    # 268 MB per layer): the headline's context length with a larger per-layer
+    # footprint.
+    L32 = 32768
+
+    def step32():
+        for layer in range(c["layers"]):
+            kv.attention_device(layer, c["heads"], q.data_ptr() + 4 * hd * layer, 1, L32 - 1,
+                                att.data_ptr() + 4 * hd * layer)
+    _, ms32 = time_launches(torch, step32, c["layers"], steps, 2)
+    b32 = decode_bytes(L32, c["heads"], c["kv_heads"], c["d"])
+    g32 = b32 / (ms32 * 1e-3) / 1e9
+    at32 = {"L": L32, "workgroups": kv.last_grid(), "bytes_per_layer": b32, "us_per_layer": round(ms32 * 1e3, 2),
+            "GBps": round(g32, 1), "pct_of_peak": round(100 * g32 / HBM_PEAK_GBS, 1)}
     kv.close()
     best = sweep[0]
     return {"workload": "Llama-3-8B shape (Hq 32 / Hkv 8, d 128), 32 layers x 65536 positions (16 GiB K+V), "
                         "one query token per layer per step, eager launches",
-            "bytes_per_layer": bytes_layer, "auto": best, "chunk_sweep": sweep}
+            "bytes_per_layer": bytes_layer, "auto": best, "chunk_sweep": sweep, "at_32k_context": at32}
 
 
 def measure_e2e():
@@ -384,6 +399,32 @@ def main():
         ms_step, ms_launch = time_launches(torch, graph.replay, c["layers"], args.steps, args.warmup)
         mode = "hip-graph"
     grid = kv.last_grid()
+
+    # The other two cache lengths of configs[1] (512 and 4096): the same cache
+    # and q rows, each layer attending over its first L positions.  Their 24-layer
+    # working sets (6.3 MB, 50 MB) fit the 256 MB Infinity Cache, so these rates
+    # are effective bandwidth, not HBM alone.
+    lengths = []
+    for L in (512, 4096, c["L"]):
+        def step_l(L=L):
+            for layer in range(c["layers"]):
+                kv.attention_device(layer, c["heads"], qp + 4 * qd * layer, 1, L - 1, ap_ + 4 * hd * layer)
+        if args.eager:
+            ms_l, _ = time_launches(torch, step_l, c["layers"], args.steps, args.warmup)
+        else:
+            g_l = torch.cuda.CUDAGraph()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g_l, stream=stream):
+                step_l()
+            torch.cuda.synchronize()
+            ms_l, _ = time_launches(torch, g_l.replay, c["layers"], args.steps, args.warmup)
+            del g_l
+        b_l = decode_bytes(L, c["heads"], c["kv_heads"], c["d"])
+        gbs = b_l * c["layers"] / (ms_l * 1e-3) / 1e9
+        lengths.append({"L": L, "us_per_step": round(ms_l * 1e3, 2), "us_per_layer": round(ms_l * 1e3 / c["layers"], 3),
+                        "GBps": round(gbs, 1), "pct_of_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+                        "workgroups": kv.last_grid(),
+                        "served_from": "HBM" if L == c["L"] else "Infinity Cache (24-layer set < 256 MB)"})
     # HBM bytes per launch measured by the committed rocprofv3 --pmc runs on this
     # same workload (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size).
     traffic = None
@@ -417,6 +458,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "wick::decode_kernel<64, false, false> + wick::decode_merge_kernel<64> (one call)", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "bytes_per_launch": bytes_layer, "us_per_launch": round(ms_launch * 1e3, 3)},
+        "decode_lengths": lengths,
     }
 
     # ---------------- prefill (configs[2] at T = 512 and 2048; configs[3] chunked)

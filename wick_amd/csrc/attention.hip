@@ -667,6 +667,164 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     prefill_split_body<128>(a);
 }
 
+// ------------------------------------------------------------------ lean head_dim-128 prefill
+//
+// On gfx950 an f32 MFMA does not overlap vector ALU work: every VALU
+// instruction a SIMD issues, from any wave, delays its MFMA pipe by about 5
+// cycles, and every global dwordx4 load whose data returns to VGPRs by about
+// 19 (measured: 1 VALU per 16x16x4 MFMA costs 16% of the matrix rate, 4 cost
+// 40%).  The split kernel above spends ~113 VALU instructions per 16-key tile
+// on 64 MFMAs.  This variant keeps the same work split and numerics contract
+// and strips the per-tile VALU work:
+//   - K/V tiles come through buffer loads: a wave-uniform resource over the kv
+//     head's first kend rows, a per-lane offset fixed for the whole loop and
+//     the tile's position in a scalar offset, so no address arithmetic runs
+//     per tile and rows past kend read as zero (no clamping);
+//   - q is pre-multiplied by scale * log2(e), so scores come out of the MFMA
+//     in log2 units and exp2 takes them directly (one extra rounding of q
+//     against the reference's dot-then-scale; outputs move by ~1e-7);
+//   - the QK products run as one accumulator chain (the MFMA pipe does not
+//     stall on dependent chains), so no partial sums;
+//   - causal / range masking only runs on tiles that reach a row's limit.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, unsigned bytes) {
+    // Wave-uniform by construction; readfirstlane keeps it in SGPRs (otherwise
+    // the compiler wraps every load in a per-lane waterfall loop).
+    const unsigned long long p = (unsigned long long)base;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)p);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(p >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(((unsigned long long)hi << 32) | lo), (short)0,
+                                             (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ f4 bload4(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    const u4 x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    return f4{__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3])};
+}
+
+// Largest cache capacity the lean kernel addresses with 32-bit buffer offsets.
+constexpr long long kLeanMaxCapacity = 0x7fffffffLL / (128 * 4);
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prefill_lean_kernel_d128(
+    const PrefillArgs a) {
+    constexpr int D = 128;
+    using S = Shape<D>;
+    __shared__ float sm_m[4][16], sm_l[4][16];
+    __shared__ float sm_o[4][16][D];
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kvh = blockIdx.x % a.kv_heads;
+    const int idx = (int)(blockIdx.x / a.kv_heads), half = (a.nblocks + 1) >> 1;
+    const int b = (a.zigzag && idx >= half) ? idx - half : a.nblocks - 1 - idx;
+    const float *Kh = a.k + (size_t)kvh * a.capacity * D;
+    const float *Vh = a.v + (size_t)kvh * a.capacity * D;
+    const int col = lane & 15, g = lane >> 4;
+    const int heads = a.kv_heads * a.group;
+    const int nrows = a.t * a.group;
+    const int r = 16 * b + col;
+    const bool valid = r < nrows;
+    const int i = valid ? r / a.group : 0, hh = valid ? r % a.group : 0;
+    const int imax = min(16 * b + 15, nrows - 1) / a.group;
+    const int kend = a.start + imax + 1;
+    const int lim = valid ? a.start + i + 1 : kend;           // padding rows see every key
+    const int lim_min = a.start + (16 * b) / a.group + 1;     // smallest limit in the block
+    const int nt = (kend + 15) >> 4;
+    const int ks = 16 * ((w * nt) >> 2), ke = min(16 * (((w + 1) * nt) >> 2), kend);
+
+    const float c = a.scale * kLog2e;
+    f4 q[S::KJ];
+    {
+        const float *row = valid ? a.q + (size_t)i * heads * D + (size_t)(kvh * a.group + hh) * D : a.q;
+        const float keep = valid ? c : 0.f;
+#pragma unroll
+        for (int j = 0; j < S::KJ; j++) q[j] = *reinterpret_cast<const f4 *>(row + 16 * j + 4 * g) * keep;
+    }
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(Kh, (unsigned)kend * D * 4u);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vh, (unsigned)kend * D * 4u);
+    // Same lane layout as load_tiles: lane (i = col, g) reads K[p0 + i][16j + 4g .. +3]
+    // and V[p0 + 4g + m][4i + 64 seg .. +3].
+    const unsigned vk = (unsigned)((col * D + 4 * g) * 4);
+    const unsigned vv = (unsigned)((4 * g * D + 4 * col) * 4);
+
+    float m = -INFINITY, mref = 0.f, l = 0.f;  // m, mref in log2 units
+    f4 o[S::DB];
+#pragma unroll
+    for (int db = 0; db < S::DB; db++) o[db] = f4{0.f, 0.f, 0.f, 0.f};
+    const int ntl = (ke - ks + 15) >> 4;
+    const int unmasked_end = min(lim_min, ke);
+    for (int n = 0; n < ntl; n++) {
+        const int p0 = ks + 16 * n;
+        const unsigned so = (unsigned)p0 * D * 4u;
+        f4 kt[S::KJ];
+#pragma unroll
+        for (int j = 0; j < S::KJ; j++) kt[j] = bload4(rk, vk + 64 * j, so);
+        f4 vt[4][2];
+#pragma unroll
+        for (int mm = 0; mm < 4; mm++)
+#pragma unroll
+            for (int seg = 0; seg < 2; seg++) vt[mm][seg] = bload4(rv, vv + mm * D * 4 + seg * 256, so);
+        f4 sacc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < S::KJ; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) sacc = mfma16x16x4(kt[j][e], q[j][e], sacc);
+        float s0 = sacc[0], s1 = sacc[1], s2 = sacc[2], s3 = sacc[3];
+        if (p0 + 16 > unmasked_end) {
+            // keys past this row's causal limit or past the wave's range
+            const int key0 = p0 + 4 * g, kl = min(lim, ke);
+            s0 = key0 + 0 < kl ? s0 : -INFINITY;
+            s1 = key0 + 1 < kl ? s1 : -INFINITY;
+            s2 = key0 + 2 < kl ? s2 : -INFINITY;
+            s3 = key0 + 3 < kl ? s3 : -INFINITY;
+        }
+        const float mnew = fmaxf(m, col_max(fmaxf(fmaxf(s0, s1), fmaxf(s2, s3))));
+        const float mr = (mnew == -INFINITY) ? 0.f : mnew;
+        const float alpha = exp2_fast(m - mr);
+        if (!__all(alpha == 1.0f)) {
+            l *= alpha;
+#pragma unroll
+            for (int db = 0; db < S::DB; db++) o[db] *= alpha;
+        }
+        m = mnew;
+        mref = mr;
+        const float e0 = exp2_fast(s0 - mref), e1 = exp2_fast(s1 - mref), e2 = exp2_fast(s2 - mref),
+                    e3 = exp2_fast(s3 - mref);
+        l += (e0 + e1) + (e2 + e3);
+        const float pe[4] = {e0, e1, e2, e3};
+#pragma unroll
+        for (int mm = 0; mm < 4; mm++)
+#pragma unroll
+            for (int db = 0; db < S::DB; db++) o[db] = mfma16x16x4(vt[mm][db >> 2][db & 3], pe[mm], o[db]);
+    }
+    l = col_sum(l);
+    if (g == 0) {
+        sm_m[w][col] = m;
+        sm_l[w][col] = l;
+    }
+#pragma unroll
+    for (int db = 0; db < S::DB; db++)
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) sm_o[w][col][out_dim<D>(g, rr, db)] = o[db][rr];
+    __syncthreads();
+    // Merge the 4 waves' states (log2 units); wave 0 holds key 0, so M is finite.
+    for (int x = threadIdx.x; x < 16 * D; x += blockDim.x) {
+        const int cc = x / D, d = x % D;
+        const int rc = 16 * b + cc;
+        if (rc >= nrows) break;
+        float M = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) M = fmaxf(M, sm_m[ww][cc]);
+        float oo = 0.f, L = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) {
+            const float e = exp2_fast(sm_m[ww][cc] - M);
+            oo += sm_o[ww][cc][d] * e;
+            L += sm_l[ww][cc] * e;
+        }
+        const int ic = rc / a.group, hc = rc % a.group;
+        a.att[(size_t)ic * heads * D + (size_t)(kvh * a.group + hc) * D + d] = oo / L;
+    }
+}
+
 // ------------------------------------------------------------------ append
 
 // src rows [t][kv_heads*D] -> cache [kv_heads][capacity][D] at start.. (the
@@ -753,7 +911,7 @@ int prefill_blocks_per_cu(int head_dim) {
     case 16: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_split_kernel<16>, 256, 0); break;
     case 32: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_split_kernel<32>, 256, 0); break;
     case 64: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_split_kernel<64>, 256, 0); break;
-    case 128: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_split_kernel_d128, 256, 0); break;
+    case 128: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_lean_kernel_d128, 256, 0); break;
     default: break;
     }
     return (e == hipSuccess && n > 0) ? n : 1;
@@ -765,7 +923,9 @@ int prefill_grid(const PrefillArgs &a) {
 
 hipError_t launch_prefill(int head_dim, const PrefillArgs &a, hipStream_t s) {
     const int grid = prefill_grid(a);
-    if (a.split && head_dim == 128) {
+    if (a.split && head_dim == 128 && a.capacity <= kLeanMaxCapacity) {
+        hipLaunchKernelGGL(prefill_lean_kernel_d128, dim3(grid), dim3(256), 0, s, a);
+    } else if (a.split && head_dim == 128) {
         hipLaunchKernelGGL(prefill_split_kernel_d128, dim3(grid), dim3(256), 0, s, a);
     } else if (a.split) {
         WICK_DISPATCH_D(head_dim, prefill_split_kernel, dim3(grid), dim3(256), 0, s, a);
