@@ -702,13 +702,19 @@ __device__ __forceinline__ f4 bload4(__amdgpu_buffer_rsrc_t r, unsigned voff, un
     return f4{__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3])};
 }
 
-// Largest cache capacity the lean kernel addresses with 32-bit buffer offsets.
-constexpr long long kLeanMaxCapacity = 0x7fffffffLL / (128 * 4);
+// Largest cache capacity the lean kernel addresses with 32-bit buffer offsets
+// (bytes of one kv head's rows must fit a signed 32-bit range).
+template <int D>
+constexpr long long lean_max_capacity() { return 0x7fffffffLL / (D * 4); }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prefill_lean_kernel_d128(
-    const PrefillArgs a) {
-    constexpr int D = 128;
+// head_dim 64 and 128.  One softmax step covers TG 16-key tiles (two at
+// head_dim 64, so that the step's fixed VALU work -- column max, rescale --
+// is spread over as many MFMAs as at head_dim 128).
+template <int D>
+__device__ __forceinline__ void prefill_lean_body(const PrefillArgs &a) {
     using S = Shape<D>;
+    static_assert(D == 64 || D == 128, "lean prefill: head_dim 64 or 128");
+    constexpr int TG = S::TG;
     __shared__ float sm_m[4][16], sm_l[4][16];
     __shared__ float sm_o[4][16][D];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -749,34 +755,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     f4 o[S::DB];
 #pragma unroll
     for (int db = 0; db < S::DB; db++) o[db] = f4{0.f, 0.f, 0.f, 0.f};
-    const int ntl = (ke - ks + 15) >> 4;
+    const int nsteps = (ke - ks + 16 * TG - 1) / (16 * TG);
     const int unmasked_end = min(lim_min, ke);
-    for (int n = 0; n < ntl; n++) {
-        const int p0 = ks + 16 * n;
-        const unsigned so = (unsigned)p0 * D * 4u;
-        f4 kt[S::KJ];
+    for (int n = 0; n < nsteps; n++) {
+        const int p0 = ks + 16 * TG * n;
+        f4 kt[TG][S::KJ];
+        f4 vt[TG][4][S::NSEG];
 #pragma unroll
-        for (int j = 0; j < S::KJ; j++) kt[j] = bload4(rk, vk + 64 * j, so);
-        f4 vt[4][2];
+        for (int u = 0; u < TG; u++) {
+            const unsigned so = (unsigned)(p0 + 16 * u) * D * 4u;
 #pragma unroll
-        for (int mm = 0; mm < 4; mm++)
+            for (int j = 0; j < S::KJ; j++) kt[u][j] = bload4(rk, vk + 64 * j, so);
 #pragma unroll
-            for (int seg = 0; seg < 2; seg++) vt[mm][seg] = bload4(rv, vv + mm * D * 4 + seg * 256, so);
-        f4 sacc = f4{0.f, 0.f, 0.f, 0.f};
+            for (int mm = 0; mm < 4; mm++)
 #pragma unroll
-        for (int j = 0; j < S::KJ; j++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) sacc = mfma16x16x4(kt[j][e], q[j][e], sacc);
-        float s0 = sacc[0], s1 = sacc[1], s2 = sacc[2], s3 = sacc[3];
-        if (p0 + 16 > unmasked_end) {
-            // keys past this row's causal limit or past the wave's range
-            const int key0 = p0 + 4 * g, kl = min(lim, ke);
-            s0 = key0 + 0 < kl ? s0 : -INFINITY;
-            s1 = key0 + 1 < kl ? s1 : -INFINITY;
-            s2 = key0 + 2 < kl ? s2 : -INFINITY;
-            s3 = key0 + 3 < kl ? s3 : -INFINITY;
+                for (int seg = 0; seg < S::NSEG; seg++) vt[u][mm][seg] = bload4(rv, vv + mm * D * 4 + seg * 256, so);
         }
-        const float mnew = fmaxf(m, col_max(fmaxf(fmaxf(s0, s1), fmaxf(s2, s3))));
+        float sc[TG][4];
+#pragma unroll
+        for (int u = 0; u < TG; u++) {
+            f4 sacc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < S::KJ; j++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) sacc = mfma16x16x4(kt[u][j][e], q[j][e], sacc);
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++) sc[u][rr] = sacc[rr];
+        }
+        if (p0 + 16 * TG > unmasked_end) {
+            // keys past this row's causal limit or past the wave's range
+            const int kl = min(lim, ke);
+#pragma unroll
+            for (int u = 0; u < TG; u++)
+#pragma unroll
+                for (int rr = 0; rr < 4; rr++) sc[u][rr] = (p0 + 16 * u + 4 * g + rr < kl) ? sc[u][rr] : -INFINITY;
+        }
+        float lm = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < TG; u++) lm = fmaxf(lm, fmaxf(fmaxf(sc[u][0], sc[u][1]), fmaxf(sc[u][2], sc[u][3])));
+        const float mnew = fmaxf(m, col_max(lm));
         const float mr = (mnew == -INFINITY) ? 0.f : mnew;
         const float alpha = exp2_fast(m - mr);
         if (!__all(alpha == 1.0f)) {
@@ -786,14 +803,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
         }
         m = mnew;
         mref = mr;
-        const float e0 = exp2_fast(s0 - mref), e1 = exp2_fast(s1 - mref), e2 = exp2_fast(s2 - mref),
-                    e3 = exp2_fast(s3 - mref);
-        l += (e0 + e1) + (e2 + e3);
-        const float pe[4] = {e0, e1, e2, e3};
+        float ls = 0.f;
 #pragma unroll
-        for (int mm = 0; mm < 4; mm++)
+        for (int u = 0; u < TG; u++)
 #pragma unroll
-            for (int db = 0; db < S::DB; db++) o[db] = mfma16x16x4(vt[mm][db >> 2][db & 3], pe[mm], o[db]);
+            for (int rr = 0; rr < 4; rr++) {
+                sc[u][rr] = exp2_fast(sc[u][rr] - mref);
+                ls += sc[u][rr];
+            }
+        l += ls;
+#pragma unroll
+        for (int u = 0; u < TG; u++)
+#pragma unroll
+            for (int mm = 0; mm < 4; mm++)
+#pragma unroll
+                for (int db = 0; db < S::DB; db++)
+                    o[db] = mfma16x16x4(vt[u][mm][db / 4][db % 4], sc[u][mm], o[db]);
     }
     l = col_sum(l);
     if (g == 0) {
@@ -824,6 +849,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
         a.att[(size_t)ic * heads * D + (size_t)(kvh * a.group + hc) * D + d] = oo / L;
     }
 }
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prefill_lean_kernel_d128(
+    const PrefillArgs a) {
+    prefill_lean_body<128>(a);
+}
+
+__global__ __launch_bounds__(256) void prefill_lean_kernel_d64(const PrefillArgs a) { prefill_lean_body<64>(a); }
 
 // ------------------------------------------------------------------ append
 
@@ -910,7 +942,7 @@ int prefill_blocks_per_cu(int head_dim) {
     switch (head_dim) {
     case 16: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_split_kernel<16>, 256, 0); break;
     case 32: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_split_kernel<32>, 256, 0); break;
-    case 64: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_split_kernel<64>, 256, 0); break;
+    case 64: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_lean_kernel_d64, 256, 0); break;
     case 128: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_lean_kernel_d128, 256, 0); break;
     default: break;
     }
@@ -923,8 +955,10 @@ int prefill_grid(const PrefillArgs &a) {
 
 hipError_t launch_prefill(int head_dim, const PrefillArgs &a, hipStream_t s) {
     const int grid = prefill_grid(a);
-    if (a.split && head_dim == 128 && a.capacity <= kLeanMaxCapacity) {
+    if (a.split && head_dim == 128 && a.capacity <= lean_max_capacity<128>()) {
         hipLaunchKernelGGL(prefill_lean_kernel_d128, dim3(grid), dim3(256), 0, s, a);
+    } else if (a.split && head_dim == 64 && a.capacity <= lean_max_capacity<64>()) {
+        hipLaunchKernelGGL(prefill_lean_kernel_d64, dim3(grid), dim3(256), 0, s, a);
     } else if (a.split && head_dim == 128) {
         hipLaunchKernelGGL(prefill_split_kernel_d128, dim3(grid), dim3(256), 0, s, a);
     } else if (a.split) {
