@@ -342,6 +342,153 @@ __device__ __forceinline__ void prep_row16(const float *src, float *dst, const f
     }
 }
 
+// ------------------------------------------------------------------ lean building blocks
+//
+// On gfx950 an f32 MFMA does not overlap vector ALU work: every VALU
+// instruction a SIMD issues, from any wave, delays its MFMA pipe by about 5
+// cycles, and every global dwordx4 load whose data returns to VGPRs by about
+// 19 (measured: 1 VALU per 16x16x4 MFMA costs 16% of the matrix rate, 4 cost
+// 40%).  The lean kernels therefore keep per-tile VALU work minimal:
+//   - K/V tiles come through buffer loads: a wave-uniform resource over the kv
+//     head's valid rows, a per-lane offset fixed for the whole loop and the
+//     tile's position in a scalar offset, so no address arithmetic runs per
+//     tile and rows past the end read as zero (no clamping);
+//   - q is pre-multiplied by scale * log2(e), so scores come out of the MFMA
+//     in log2 units and exp2 takes them directly (one extra rounding of q
+//     against the reference's dot-then-scale; outputs move by ~1e-7);
+//   - the QK products run as one accumulator chain (the MFMA pipe does not
+//     stall on dependent chains), so no partial sums;
+//   - masking only runs on groups that reach a limit.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, unsigned bytes) {
+    // Wave-uniform by construction; readfirstlane keeps it in SGPRs (otherwise
+    // the compiler wraps every load in a per-lane waterfall loop).
+    const unsigned long long p = (unsigned long long)base;
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)p);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(p >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(((unsigned long long)hi << 32) | lo), (short)0,
+                                             (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ f4 bload4(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    const u4 x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    return f4{__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3])};
+}
+
+// A group of TG 16-key tiles for the lean kernels, in the lane layout of
+// load_tiles: lane (i = col, g) holds K[p0 + i][16j + 4g .. +3] and
+// V[p0 + 4g + m][4i + 64 seg .. +3] (head_dim 64 and 128).
+template <int D>
+struct LeanGroup {
+    f4 k[Shape<D>::TG][Shape<D>::KJ];
+    f4 v[Shape<D>::TG][4][Shape<D>::NSEG];
+};
+
+// Buffer loads of the group starting at key p0 of the resource's kv head.
+// vk, vv: the lane's fixed byte offsets (see lean_lane_offsets); rows past the
+// resource's end read as zero.
+template <int D>
+__device__ __forceinline__ void lean_load(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, unsigned vk,
+                                          unsigned vv, int p0, LeanGroup<D> &t) {
+    using S = Shape<D>;
+#pragma unroll
+    for (int u = 0; u < S::TG; u++) {
+        const unsigned so = (unsigned)(p0 + 16 * u) * D * 4u;
+#pragma unroll
+        for (int j = 0; j < S::KJ; j++) t.k[u][j] = bload4(rk, vk + 64 * j, so);
+#pragma unroll
+        for (int mm = 0; mm < 4; mm++)
+#pragma unroll
+            for (int seg = 0; seg < S::NSEG; seg++) t.v[u][mm][seg] = bload4(rv, vv + mm * D * 4 + seg * 256, so);
+    }
+}
+
+// The same group through plain global loads from the kv head's rows, rows
+// clamped to kend - 1 when `clamp` (the last group of a range).  Streaming
+// from HBM these run faster than buffer loads (config 2 decode split kernel:
+// 8.5 against 9.2 us).
+template <int D>
+__device__ __forceinline__ void lean_load_global(const float *__restrict__ Kh, const float *__restrict__ Vh, int p0,
+                                                 int kend, bool clamp, int lane, LeanGroup<D> &t) {
+    using S = Shape<D>;
+    const int col = lane & 15, g = lane >> 4;
+    const int last = clamp ? kend - 1 : 0x7fffffff;
+#pragma unroll
+    for (int u = 0; u < S::TG; u++) {
+        const float *kr = Kh + (size_t)min(p0 + 16 * u + col, last) * D + 4 * g;
+#pragma unroll
+        for (int j = 0; j < S::KJ; j++) t.k[u][j] = *reinterpret_cast<const f4 *>(kr + 16 * j);
+#pragma unroll
+        for (int mm = 0; mm < 4; mm++) {
+            const float *vr = Vh + (size_t)min(p0 + 16 * u + 4 * g + mm, last) * D + 4 * col;
+#pragma unroll
+            for (int seg = 0; seg < S::NSEG; seg++) t.v[u][mm][seg] = *reinterpret_cast<const f4 *>(vr + 64 * seg);
+        }
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void lean_lane_offsets(int lane, unsigned &vk, unsigned &vv) {
+    const int col = lane & 15, g = lane >> 4;
+    vk = (unsigned)((col * D + 4 * g) * 4);
+    vv = (unsigned)((4 * g * D + 4 * col) * 4);
+}
+
+// One online-softmax step over a loaded group.  q is pre-scaled by
+// scale * log2(e), so scores, m and mref are in log2 units.  When `masked`,
+// keys at or past this lane's klimit get -inf.
+template <int D>
+__device__ __forceinline__ void lean_step(const LeanGroup<D> &t, const f4 (&q)[Shape<D>::KJ], int p0, bool masked,
+                                          int klimit, int g, float &m, float &mref, float &l, f4 (&o)[Shape<D>::DB]) {
+    using S = Shape<D>;
+    constexpr int TG = S::TG;
+    float sc[TG][4];
+#pragma unroll
+    for (int u = 0; u < TG; u++) {
+        f4 sacc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < S::KJ; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) sacc = mfma16x16x4(t.k[u][j][e], q[j][e], sacc);
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) sc[u][rr] = sacc[rr];
+    }
+    if (masked) {
+#pragma unroll
+        for (int u = 0; u < TG; u++)
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++) sc[u][rr] = (p0 + 16 * u + 4 * g + rr < klimit) ? sc[u][rr] : -INFINITY;
+    }
+    float lm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < TG; u++) lm = fmaxf(lm, fmaxf(fmaxf(sc[u][0], sc[u][1]), fmaxf(sc[u][2], sc[u][3])));
+    const float mnew = fmaxf(m, col_max(lm));
+    const float mr = (mnew == -INFINITY) ? 0.f : mnew;
+    const float alpha = exp2_fast(m - mr);
+    if (!__all(alpha == 1.0f)) {
+        l *= alpha;
+#pragma unroll
+        for (int db = 0; db < S::DB; db++) o[db] *= alpha;
+    }
+    m = mnew;
+    mref = mr;
+    float ls = 0.f;
+#pragma unroll
+    for (int u = 0; u < TG; u++)
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+            sc[u][rr] = exp2_fast(sc[u][rr] - mref);
+            ls += sc[u][rr];
+        }
+    l += ls;
+#pragma unroll
+    for (int u = 0; u < TG; u++)
+#pragma unroll
+        for (int mm = 0; mm < 4; mm++)
+#pragma unroll
+            for (int db = 0; db < S::DB; db++) o[db] = mfma16x16x4(t.v[u][mm][db / 4][db % 4], sc[u][mm], o[db]);
+}
+
 // ------------------------------------------------------------------ decode
 
 // Partial states of the split-K decode, per (unit, column): O [units][16][256][D],
@@ -426,8 +573,46 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     }
 
     WaveState<D> st;
-    init_state<D>(st);
-    attend_range<D, PP>(Kh, Vh, kbeg, kend, w * S::TG, 4 * S::TG, a.len, a.scale, q, lane, st);
+    if constexpr (D >= 64) {
+        // Lean core: q in log2 units, tiles through global loads (keys past
+        // kend clamped and masked in the chunk's last group).
+#pragma unroll
+        for (int j = 0; j < S::KJ; j++) q[j] *= a.scale * kLog2e;
+        float mref = 0.f;
+        st.m = -INFINITY;
+        st.l = 0.f;
+#pragma unroll
+        for (int db = 0; db < S::DB; db++) st.o[db] = f4{0.f, 0.f, 0.f, 0.f};
+        constexpr int GK = 16 * S::TG;                 // keys per group
+        const int wbeg = __builtin_amdgcn_readfirstlane(kbeg + GK * w), step = 4 * GK;
+        if constexpr (PP) {
+            // the next group's loads go out before this group's products
+            LeanGroup<D> ta, tb;
+            int p0 = wbeg;
+            if (p0 < kend) lean_load_global<D>(Kh, Vh, p0, kend, p0 + GK > kend, lane, ta);
+            while (p0 < kend) {
+                const int p1 = p0 + step;
+                if (p1 < kend) lean_load_global<D>(Kh, Vh, p1, kend, p1 + GK > kend, lane, tb);
+                lean_step<D>(ta, q, p0, p0 + GK > kend, kend, g, st.m, mref, st.l, st.o);
+                if (p1 >= kend) break;
+                const int p2 = p1 + step;
+                if (p2 < kend) lean_load_global<D>(Kh, Vh, p2, kend, p2 + GK > kend, lane, ta);
+                lean_step<D>(tb, q, p1, p1 + GK > kend, kend, g, st.m, mref, st.l, st.o);
+                p0 = p2;
+            }
+        } else {
+            for (int p0 = wbeg; p0 < kend; p0 += step) {
+                LeanGroup<D> t;
+                const bool tail = p0 + GK > kend;
+                lean_load_global<D>(Kh, Vh, p0, kend, tail, lane, t);
+                lean_step<D>(t, q, p0, tail, kend, g, st.m, mref, st.l, st.o);
+            }
+        }
+    } else {
+        init_state<D>(st);
+        attend_range<D, PP>(Kh, Vh, kbeg, kend, w * S::TG, 4 * S::TG, a.len, a.scale, q, lane, st);
+        st.m *= kLog2e;  // the merges take maxima in log2 units
+    }
     st.l = col_sum(st.l);
 
     if (g == 0) {
@@ -440,8 +625,8 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
         for (int r = 0; r < 4; r++) sm_o[w][col][out_dim<D>(g, r, db)] = st.o[db][r];
     __syncthreads();
 
-    // Merge the 4 waves of this workgroup.  Wave 0 always holds the chunk's
-    // first key, so the merged max is finite.
+    // Merge the 4 waves of this workgroup (maxima in log2 units).  Wave 0
+    // always holds the chunk's first key, so the merged max is finite.
     const DecodeSpace<D> ws(a.part, units);
     for (int idx = threadIdx.x; idx < ncols * D; idx += blockDim.x) {
         const int c = idx / D, d = idx % D;
@@ -451,7 +636,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
         float o = 0.f, L = 0.f;
 #pragma unroll
         for (int ww = 0; ww < 4; ww++) {
-            const float e = exp2_fast((sm_m[ww][c] - M) * kLog2e);
+            const float e = exp2_fast(sm_m[ww][c] - M);
             o += sm_o[ww][c][d] * e;
             L += sm_l[ww][c] * e;
         }
@@ -468,7 +653,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     }
 }
 
-// Merge pass: workgroup (query head, 16-dim slice) combines the nchunks
+// Merge pass (maxima in log2 units): workgroup (query head, 16-dim slice) combines the nchunks
 // (<= 256) partial states of one query head for 16 of its head dims; the grid
 // holds exactly heads x D/16 workgroups.  Thread
 // (grp, dd) of 16 groups owns children grp, grp + 16, ...: it loads their O, m
@@ -510,7 +695,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
     float acc = 0.f, L = 0.f;
 #pragma unroll
     for (int u = 0; u < NB; u++) {
-        const float e = exp2_fast((vm[u] - Mref) * kLog2e);
+        const float e = exp2_fast(vm[u] - Mref);
         acc += vo[u] * e;
         L += vl[u] * e;
     }
@@ -525,7 +710,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
         float ot = 0.f, Lt = 0.f;
 #pragma unroll
         for (int gg = 0; gg < G; gg++) {
-            const float e = exp2_fast((sm[gg][tid] - Mt) * kLog2e);  // 0 for empty groups
+            const float e = exp2_fast(sm[gg][tid] - Mt);  // 0 for empty groups
             ot += so[gg][tid] * e;
             Lt += sl[gg][tid] * e;
         }
@@ -667,41 +852,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
     prefill_split_body<128>(a);
 }
 
-// ------------------------------------------------------------------ lean head_dim-128 prefill
+// ------------------------------------------------------------------ lean prefill
 //
-// On gfx950 an f32 MFMA does not overlap vector ALU work: every VALU
-// instruction a SIMD issues, from any wave, delays its MFMA pipe by about 5
-// cycles, and every global dwordx4 load whose data returns to VGPRs by about
-// 19 (measured: 1 VALU per 16x16x4 MFMA costs 16% of the matrix rate, 4 cost
-// 40%).  The split kernel above spends ~113 VALU instructions per 16-key tile
-// on 64 MFMAs.  This variant keeps the same work split and numerics contract
-// and strips the per-tile VALU work:
-//   - K/V tiles come through buffer loads: a wave-uniform resource over the kv
-//     head's first kend rows, a per-lane offset fixed for the whole loop and
-//     the tile's position in a scalar offset, so no address arithmetic runs
-//     per tile and rows past kend read as zero (no clamping);
-//   - q is pre-multiplied by scale * log2(e), so scores come out of the MFMA
-//     in log2 units and exp2 takes them directly (one extra rounding of q
-//     against the reference's dot-then-scale; outputs move by ~1e-7);
-//   - the QK products run as one accumulator chain (the MFMA pipe does not
-//     stall on dependent chains), so no partial sums;
-//   - causal / range masking only runs on tiles that reach a row's limit.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, unsigned bytes) {
-    // Wave-uniform by construction; readfirstlane keeps it in SGPRs (otherwise
-    // the compiler wraps every load in a per-lane waterfall loop).
-    const unsigned long long p = (unsigned long long)base;
-    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)p);
-    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(p >> 32));
-    return __builtin_amdgcn_make_buffer_rsrc((void *)(((unsigned long long)hi << 32) | lo), (short)0,
-                                             (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
-}
-
-__device__ __forceinline__ f4 bload4(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
-    typedef unsigned u4 __attribute__((ext_vector_type(4)));
-    const u4 x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
-    return f4{__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3])};
-}
-
+// The split kernel above spends ~113 VALU instructions per 16-key tile on 64
+// MFMAs at head_dim 128.  The lean variant keeps its work split (16-row
+// block per workgroup, keys split over the 4 waves, heaviest blocks first)
+// and runs each tile through lean_load / lean_step (~30 VALU per tile).
 // Largest cache capacity the lean kernel addresses with 32-bit buffer offsets
 // (bytes of one kv head's rows must fit a signed 32-bit range).
 template <int D>
@@ -746,10 +902,8 @@ __device__ __forceinline__ void prefill_lean_body(const PrefillArgs &a) {
     }
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(Kh, (unsigned)kend * D * 4u);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vh, (unsigned)kend * D * 4u);
-    // Same lane layout as load_tiles: lane (i = col, g) reads K[p0 + i][16j + 4g .. +3]
-    // and V[p0 + 4g + m][4i + 64 seg .. +3].
-    const unsigned vk = (unsigned)((col * D + 4 * g) * 4);
-    const unsigned vv = (unsigned)((4 * g * D + 4 * col) * 4);
+    unsigned vk, vv;
+    lean_lane_offsets<D>(lane, vk, vv);
 
     float m = -INFINITY, mref = 0.f, l = 0.f;  // m, mref in log2 units
     f4 o[S::DB];
@@ -757,68 +911,13 @@ __device__ __forceinline__ void prefill_lean_body(const PrefillArgs &a) {
     for (int db = 0; db < S::DB; db++) o[db] = f4{0.f, 0.f, 0.f, 0.f};
     const int nsteps = (ke - ks + 16 * TG - 1) / (16 * TG);
     const int unmasked_end = min(lim_min, ke);
+    const int klimit = min(lim, ke);
     for (int n = 0; n < nsteps; n++) {
         const int p0 = ks + 16 * TG * n;
-        f4 kt[TG][S::KJ];
-        f4 vt[TG][4][S::NSEG];
-#pragma unroll
-        for (int u = 0; u < TG; u++) {
-            const unsigned so = (unsigned)(p0 + 16 * u) * D * 4u;
-#pragma unroll
-            for (int j = 0; j < S::KJ; j++) kt[u][j] = bload4(rk, vk + 64 * j, so);
-#pragma unroll
-            for (int mm = 0; mm < 4; mm++)
-#pragma unroll
-                for (int seg = 0; seg < S::NSEG; seg++) vt[u][mm][seg] = bload4(rv, vv + mm * D * 4 + seg * 256, so);
-        }
-        float sc[TG][4];
-#pragma unroll
-        for (int u = 0; u < TG; u++) {
-            f4 sacc = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int j = 0; j < S::KJ; j++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) sacc = mfma16x16x4(kt[u][j][e], q[j][e], sacc);
-#pragma unroll
-            for (int rr = 0; rr < 4; rr++) sc[u][rr] = sacc[rr];
-        }
-        if (p0 + 16 * TG > unmasked_end) {
-            // keys past this row's causal limit or past the wave's range
-            const int kl = min(lim, ke);
-#pragma unroll
-            for (int u = 0; u < TG; u++)
-#pragma unroll
-                for (int rr = 0; rr < 4; rr++) sc[u][rr] = (p0 + 16 * u + 4 * g + rr < kl) ? sc[u][rr] : -INFINITY;
-        }
-        float lm = -INFINITY;
-#pragma unroll
-        for (int u = 0; u < TG; u++) lm = fmaxf(lm, fmaxf(fmaxf(sc[u][0], sc[u][1]), fmaxf(sc[u][2], sc[u][3])));
-        const float mnew = fmaxf(m, col_max(lm));
-        const float mr = (mnew == -INFINITY) ? 0.f : mnew;
-        const float alpha = exp2_fast(m - mr);
-        if (!__all(alpha == 1.0f)) {
-            l *= alpha;
-#pragma unroll
-            for (int db = 0; db < S::DB; db++) o[db] *= alpha;
-        }
-        m = mnew;
-        mref = mr;
-        float ls = 0.f;
-#pragma unroll
-        for (int u = 0; u < TG; u++)
-#pragma unroll
-            for (int rr = 0; rr < 4; rr++) {
-                sc[u][rr] = exp2_fast(sc[u][rr] - mref);
-                ls += sc[u][rr];
-            }
-        l += ls;
-#pragma unroll
-        for (int u = 0; u < TG; u++)
-#pragma unroll
-            for (int mm = 0; mm < 4; mm++)
-#pragma unroll
-                for (int db = 0; db < S::DB; db++)
-                    o[db] = mfma16x16x4(vt[u][mm][db / 4][db % 4], sc[u][mm], o[db]);
+        LeanGroup<D> t;
+        lean_load<D>(rk, rv, vk, vv, p0, t);
+        // keys past this row's causal limit or past the wave's range
+        lean_step<D>(t, q, p0, p0 + 16 * TG > unmasked_end, klimit, g, m, mref, l, o);
     }
     l = col_sum(l);
     if (g == 0) {
