@@ -191,6 +191,18 @@ def test_prefill_bit_stable():
     assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_prefill_beyond_lean_range_takes_split_kernel(d):
+    """A cache whose kv-head rows span more than a signed 32-bit byte range
+    (capacity > (2^31 - 1) / (4 d), ~2.1 GB of K per kv head) is past the lean
+    prefill kernel's buffer offsets; the launcher falls back to the split
+    kernel, which must agree with the oracle as well."""
+    cap = 0x7FFFFFFF // (4 * d) + 64
+    t, start = 48, 16
+    q, k, v = make_inputs(900 + d, t, start, 4, 1, d)
+    check(q, k, v, t, start, 4, 1, d, capacity=cap)
+
+
 def test_incremental_chunks_match_one_batch():
     """The tests/tiny_models.rs:73-95 property on the device cache: chunks vs one batch."""
     heads, kvh, d = 4, 2, 32
