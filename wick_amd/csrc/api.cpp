@@ -131,9 +131,9 @@ int plan_decode(wick_hip_kv *kv, int layer, int group, int len, const float *q_d
     if (rc) return rc;
     int chunk = kv->decode_chunk;
     if (chunk <= 0 && len <= wick::kDecodeSingleChunkMax) {
-        // Short context: one workgroup per unit and no merge pass.  Its 4
-        // waves take at most two 32-key groups each, which costs less
-        // than the second launch a split needs.
+        // Short context: one workgroup per unit and no merge pass.  Its
+        // waves (8 at head_dim <= 64, else 4) take at most two tile groups
+        // each, which costs less than the second launch a split needs.
         chunk = len;
     } else if (chunk <= 0) {
         // One resident round: as many chunks as the GPU holds decode

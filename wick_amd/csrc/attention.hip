@@ -524,11 +524,14 @@ struct DecodeSpace {
 // takes at most one group (short chunks) the second buffer only costs
 // registers -- 184 against 87 VGPRs at head_dim 64 -- so the launcher picks
 // the single-buffered instance then.
-template <int D, bool PREP, bool PP = (D < 128)>
-__global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
+// NW: waves per workgroup -- 4 for the split schedule; 8 (head_dim <= 64) for
+// a single chunk per unit, so that short contexts give each wave at most one
+// or two tile groups instead of two to four.
+template <int D, bool PREP, bool PP = (D < 128), int NW = 4>
+__global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
     using S = Shape<D>;
-    __shared__ float sm_m[4][16], sm_l[4][16];
-    __shared__ float sm_o[4][16][D];
+    __shared__ float sm_m[NW][16], sm_l[NW][16];
+    __shared__ float sm_o[NW][16][D];
     __shared__ float sq[PREP ? 16 : 1][D];  // prepared q rows (PREP)
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -555,7 +558,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
         const float *cr = a.rope_cos + (size_t)pos * (D / 2), *sr = a.rope_sin + (size_t)pos * (D / 2);
         float *Kw = a.k + ((size_t)kvh * a.capacity + pos) * D;
         float *Vw = a.v + ((size_t)kvh * a.capacity + pos) * D;
-        for (int r = w * 4 + (lane >> 4); r < nrows; r += 16) {
+        for (int r = w * 4 + (lane >> 4); r < nrows; r += 4 * NW) {
             if (r < ncols)
                 prep_row16<D>(a.q + (size_t)(head0 + r) * D, sq[r], a.bq ? a.bq + (size_t)(head0 + r) * D : nullptr, a.qn,
                               a.eps, cr, sr, lane & 15, lane & 48);
@@ -584,7 +587,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
         for (int db = 0; db < S::DB; db++) st.o[db] = f4{0.f, 0.f, 0.f, 0.f};
         constexpr int GK = 16 * S::TG;                 // keys per group
-        const int wbeg = __builtin_amdgcn_readfirstlane(kbeg + GK * w), step = 4 * GK;
+        const int wbeg = __builtin_amdgcn_readfirstlane(kbeg + GK * w), step = NW * GK;
         if constexpr (PP) {
             // the next group's loads go out before this group's products
             LeanGroup<D> ta, tb;
@@ -610,7 +613,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
         }
     } else {
         init_state<D>(st);
-        attend_range<D, PP>(Kh, Vh, kbeg, kend, w * S::TG, 4 * S::TG, a.len, a.scale, q, lane, st);
+        attend_range<D, PP>(Kh, Vh, kbeg, kend, w * S::TG, NW * S::TG, a.len, a.scale, q, lane, st);
         st.m *= kLog2e;  // the merges take maxima in log2 units
     }
     st.l = col_sum(st.l);
@@ -625,17 +628,17 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
         for (int r = 0; r < 4; r++) sm_o[w][col][out_dim<D>(g, r, db)] = st.o[db][r];
     __syncthreads();
 
-    // Merge the 4 waves of this workgroup (maxima in log2 units).  Wave 0
+    // Merge the NW waves of this workgroup (maxima in log2 units).  Wave 0
     // always holds the chunk's first key, so the merged max is finite.
     const DecodeSpace<D> ws(a.part, units);
     for (int idx = threadIdx.x; idx < ncols * D; idx += blockDim.x) {
         const int c = idx / D, d = idx % D;
         float M = -INFINITY;
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) M = fmaxf(M, sm_m[ww][c]);
+        for (int ww = 0; ww < NW; ww++) M = fmaxf(M, sm_m[ww][c]);
         float o = 0.f, L = 0.f;
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) {
+        for (int ww = 0; ww < NW; ww++) {
             const float e = exp2_fast(sm_m[ww][c] - M);
             o += sm_o[ww][c][d] * e;
             L += sm_l[ww][c] * e;
@@ -1003,6 +1006,21 @@ int decode_blocks_per_cu(int head_dim) {
 
 template <int D>
 void launch_decode_d(const DecodeArgs &a, int grid, hipStream_t s) {
+    if constexpr (D <= 64) {
+        if (a.nchunks == 1 && a.chunk > 4 * Shape<D>::TG * 16) {
+            // one chunk per unit: 8 waves, each with at most one or two groups
+            const bool one8 = a.chunk <= 8 * Shape<D>::TG * 16;
+            if (a.prep && one8)
+                hipLaunchKernelGGL((decode_kernel<D, true, false, 8>), dim3(grid), dim3(512), 0, s, a);
+            else if (a.prep)
+                hipLaunchKernelGGL((decode_kernel<D, true, true, 8>), dim3(grid), dim3(512), 0, s, a);
+            else if (one8)
+                hipLaunchKernelGGL((decode_kernel<D, false, false, 8>), dim3(grid), dim3(512), 0, s, a);
+            else
+                hipLaunchKernelGGL((decode_kernel<D, false, true, 8>), dim3(grid), dim3(512), 0, s, a);
+            return;
+        }
+    }
     // each of the 4 waves takes groups of TG 16-key tiles, stepping by 4 groups
     const bool one_group = a.chunk <= 4 * Shape<D>::TG * 16;
     if constexpr (D < 128) {

@@ -11,7 +11,9 @@ namespace wick {
 
 // Most split-K chunks one decode call uses per (kv head, 16-head slice).
 constexpr int kDecodeMaxChunks = 256;
-// Longest context the automatic decode schedule serves with one chunk per unit.
+// Longest context the automatic decode schedule serves with one chunk per unit
+// (config 2 at 512 positions: 10.1 us as one 8-wave chunk per kv head against
+// 7.0 us split over 16 workgroups plus the merge).
 constexpr int kDecodeSingleChunkMax = 192;
 constexpr int kTileRows = 16;  // query rows (or heads) per MFMA column block
 
