@@ -656,21 +656,35 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
     }
 }
 
-// Merge pass (maxima in log2 units): workgroup (query head, 16-dim slice) combines the nchunks
-// (<= 256) partial states of one query head for 16 of its head dims; the grid
-// holds exactly heads x D/16 workgroups.  Thread
-// (grp, dd) of 16 groups owns children grp, grp + 16, ...: it loads their O, m
-// and l together (one memory round trip), merges them by log-sum-exp against
-// its own running max, and a single LDS step combines the 16 group states the
-// same way.  Child order within a thread and group order in the combine are
-// fixed: deterministic for a given nchunks.
+// Log-sum-exp combine of two (max, O, sum) states handed over as swapped
+// pairs; symmetric in the pair, and a pair of empty states (-inf maxima)
+// stays empty.
+template <typename P>
+__device__ __forceinline__ void merge_pair(P pm, P po, P pl, float &M, float &acc, float &L) {
+    const float m0 = __uint_as_float(pm[0]), m1 = __uint_as_float(pm[1]);
+    const float M2 = fmaxf(m0, m1);
+    const float Mr = (M2 == -INFINITY) ? 0.f : M2;
+    const float e0 = exp2_fast(m0 - Mr), e1 = exp2_fast(m1 - Mr);
+    acc = __uint_as_float(po[0]) * e0 + __uint_as_float(po[1]) * e1;
+    L = __uint_as_float(pl[0]) * e0 + __uint_as_float(pl[1]) * e1;
+    M = M2;
+}
+
+// Merge pass (maxima in log2 units): workgroup (query head, 16-dim slice)
+// combines the nchunks (<= 256) partial states of one query head for 16 of its
+// head dims; the grid holds exactly heads x D/16 workgroups.  Thread (grp, dd)
+// of 16 groups owns children grp, grp + 16, ...: it loads their O, m and l
+// together (one memory round trip) and merges them by log-sum-exp against its
+// own running max; the 4 groups of each wave then combine pairwise in
+// registers and the 4 wave states in one LDS step.  Child order within a
+// thread and the combine tree are fixed: deterministic for a given nchunks.
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
     constexpr int DW = 16;                        // head dims per workgroup
     constexpr int NS = D / DW;                    // slices per column
     constexpr int G = 256 / DW;                   // thread groups over children
     constexpr int NB = kDecodeMaxChunks / G;      // children per thread
-    __shared__ float sm[G][DW], so[G][DW], sl[G][DW];
+    __shared__ float sm[4][DW], so[4][DW], sl[4][DW];
     const int units = a.kv_heads * a.hslices;
     const int ds = blockIdx.x % NS, head = blockIdx.x / NS;
     const int kvh = head / a.group, hh = head % a.group;
@@ -702,20 +716,33 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
         acc += vo[u] * e;
         L += vl[u] * e;
     }
-    sm[grp][dd] = M;
-    so[grp][dd] = acc;
-    sl[grp][dd] = L;
+    // The 4 groups of a wave (lanes l, l^16, l^32, l^48 hold the same head
+    // dim) combine in registers, pairwise through permlane swaps; both lanes
+    // of a pair compute the same bits (the combine is symmetric).  Then the 4
+    // wave states meet in LDS.
+    merge_pair(__builtin_amdgcn_permlane16_swap(__float_as_uint(M), __float_as_uint(M), false, false),
+               __builtin_amdgcn_permlane16_swap(__float_as_uint(acc), __float_as_uint(acc), false, false),
+               __builtin_amdgcn_permlane16_swap(__float_as_uint(L), __float_as_uint(L), false, false), M, acc, L);
+    merge_pair(__builtin_amdgcn_permlane32_swap(__float_as_uint(M), __float_as_uint(M), false, false),
+               __builtin_amdgcn_permlane32_swap(__float_as_uint(acc), __float_as_uint(acc), false, false),
+               __builtin_amdgcn_permlane32_swap(__float_as_uint(L), __float_as_uint(L), false, false), M, acc, L);
+    const int w = tid >> 6;
+    if ((tid & 63) < DW) {
+        sm[w][dd] = M;
+        so[w][dd] = acc;
+        sl[w][dd] = L;
+    }
     __syncthreads();
     if (tid < DW) {
         float Mt = -INFINITY;
 #pragma unroll
-        for (int gg = 0; gg < G; gg++) Mt = fmaxf(Mt, sm[gg][tid]);
+        for (int ww = 0; ww < 4; ww++) Mt = fmaxf(Mt, sm[ww][tid]);
         float ot = 0.f, Lt = 0.f;
 #pragma unroll
-        for (int gg = 0; gg < G; gg++) {
-            const float e = exp2_fast(sm[gg][tid] - Mt);  // 0 for empty groups
-            ot += so[gg][tid] * e;
-            Lt += sl[gg][tid] * e;
+        for (int ww = 0; ww < 4; ww++) {
+            const float e = exp2_fast(sm[ww][tid] - Mt);
+            ot += so[ww][tid] * e;
+            Lt += sl[ww][tid] * e;
         }
         a.att[(size_t)head * D + ds * DW + tid] = ot / Lt;
     }
