@@ -6,10 +6,11 @@
 // with scale = 1/sqrt(head_dim) (src/model.rs:527) and kv head h/group
 // (src/model.rs:526,532).
 //
-// Both kernels are built on one wave-level core (attend_range): a wave owns 16
-// "columns" -- 16 query heads of one kv head (decode) or 16 flattened
-// (token, head) rows of one kv head (prefill) -- and streams 16-key tiles of K
-// and V through two f32 MFMAs:
+// All kernels share one wave-level layout: a wave owns 16 "columns" -- 16
+// query heads of one kv head (decode) or 16 flattened (token, head) rows of
+// one kv head (prefill) -- and streams 16-key tiles of K and V through two f32
+// MFMAs (the lean core lean_load/lean_step at head_dim 64 and 128, the older
+// attend_range core at head_dim 16 and 32):
 //   S^T[16 keys x 16 cols] = K_tile[16 x D] . Q^T[D x 16]       (v_mfma_f32_16x16x4_f32)
 //   O^T[D x 16 cols]      += V_tile^T[D x 16] . P^T[16 x 16]     (same instruction)
 // so each lane owns one column: the online-softmax max/sum of a column needs
