@@ -68,6 +68,15 @@ def test_decode_lengths_and_head_dims(L, d):
     check(q, k, v, 1, L - 1, 9, 3, d)
 
 
+@pytest.mark.parametrize("L", [129, 160, 192])
+@pytest.mark.parametrize("heads,kv_heads", [(40, 2), (9, 3), (14, 2)])
+def test_decode_one_wide_chunk(L, heads, kv_heads):
+    """129..192 positions at head_dim 64 run as one chunk per unit on an 8-wave
+    workgroup (no merge pass)."""
+    q, k, v = make_inputs(L + heads, 1, L - 1, heads, kv_heads, 64)
+    check(q, k, v, 1, L - 1, heads, kv_heads, 64)
+
+
 @pytest.mark.parametrize("chunk", [64, 128, 192, 256, 1024, 4096, 8192])
 def test_decode_chunk_sizes(chunk):
     # chunk counts from 1 (no merge pass) up to 128

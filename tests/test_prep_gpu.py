@@ -91,6 +91,13 @@ def test_decode_prep_with_head_slices():
     run_chunks(40, 2, 64, [300, 1], 1e4, bias=True, norm=True)
 
 
+@pytest.mark.parametrize("heads,kv_heads", [(40, 2), (9, 3), (14, 2)])
+def test_decode_prep_one_wide_chunk(heads, kv_heads):
+    # 141..142 positions at head_dim 64: one chunk per unit on an 8-wave
+    # workgroup (group 20 also splits into two head slices per kv head)
+    run_chunks(heads, kv_heads, 64, [140, 1, 1], 1e4, bias=True, norm=True)
+
+
 def test_qwen2_shape_bias_chunked_then_decode():
     run_chunks(14, 2, 64, [37, 100, 1, 1], 1e6, bias=True, norm=False)
 
