@@ -66,7 +66,8 @@ const char *wick_hip_last_error(void);
 
 /* ---- device-resident variants (no counterpart in the reference: they let a
  *      caller whose q / k / v / att already live in HBM skip the host copies).
- *      Asynchronous on the handle's stream. */
+ *      Asynchronous on the handle's stream.  Device arrays must be 16-byte
+ *      aligned (the kernels move them as float4); others give WICK_HIP_EINVAL. */
 
 /* As wick_hip_kv_append, with k_dev / v_dev device arrays [t][kv_heads*head_dim]. */
 int wick_hip_kv_append_device(wick_hip_kv *kv, int layer, int start, int t, const float *k_dev, const float *v_dev);
@@ -106,8 +107,8 @@ int wick_hip_kv_set_prep(wick_hip_kv *kv, int layer, int heads, const float *bq,
 int wick_hip_attend(wick_hip_kv *kv, int layer, int heads, const float *q, const float *k, const float *v, int t,
                     int start, float *att);
 
-/* As wick_hip_attend on device arrays; q_dev is rewritten in place with the
- * prepared q.  Asynchronous on the handle's stream. */
+/* As wick_hip_attend on device arrays (16-byte aligned); q_dev is rewritten
+ * in place with the prepared q.  Asynchronous on the handle's stream. */
 int wick_hip_attend_device(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev,
                            const float *v_dev, int t, int start, float *att_dev);
 

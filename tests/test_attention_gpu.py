@@ -243,6 +243,15 @@ def test_errors_are_reported():
             kv.append(0, 60, np.zeros((5, 128), np.float32), np.zeros((5, 128), np.float32))
         with pytest.raises(_native.WickHipError):
             kv.set_option(_native.OPT_DECODE_CHUNK, 100)
+        # device arrays move as float4: a pointer off a 16-byte boundary is refused
+        import torch
+        qd = torch.zeros(4 * 64 + 4, dtype=torch.float32, device="cuda")
+        att = torch.zeros(4 * 64 + 4, dtype=torch.float32, device="cuda")
+        with pytest.raises(_native.WickHipError) as e:
+            kv.attention_device(0, 4, qd.data_ptr() + 4, 1, 0, att.data_ptr())
+        assert e.value.code == _native.EINVAL and "aligned" in str(e.value)
+        with pytest.raises(_native.WickHipError):
+            kv.attention_device(0, 4, qd.data_ptr(), 1, 0, att.data_ptr() + 8)
 
 
 def test_decode_hip_graph_replays_match_eager():

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdint>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -110,6 +111,12 @@ int ensure_workspace(wick_hip_kv *kv, int units) {
 int check_kv(const wick_hip_kv *kv, int layer) {
     if (!kv) return fail(WICK_HIP_EINVAL, "null cache handle");
     if (layer < 0 || layer >= kv->layers) return fail(WICK_HIP_EINVAL, "layer %d out of range [0, %d)", layer, kv->layers);
+    return WICK_HIP_OK;
+}
+
+// Device arrays handed in by the caller are read and written as float4.
+int check_aligned(const void *p, const char *what) {
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return fail(WICK_HIP_EINVAL, "%s is not 16-byte aligned", what);
     return WICK_HIP_OK;
 }
 
@@ -312,6 +319,9 @@ int attend_model(wick_hip_kv *kv, int layer, int heads, float *q_dev, const floa
     if (rc) return rc;
     if ((rc = check_span(kv, start, t))) return rc;
     if (!q_dev || !k_dev || !v_dev || !att_dev) return fail(WICK_HIP_EINVAL, "null q, k, v or att");
+    if ((rc = check_aligned(q_dev, "q_dev")) || (rc = check_aligned(k_dev, "k_dev")) ||
+        (rc = check_aligned(v_dev, "v_dev")) || (rc = check_aligned(att_dev, "att_dev")))
+        return rc;
     if (heads < 1 || heads % kv->kv_heads != 0)
         return fail(WICK_HIP_EINVAL, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv->kv_heads);
     if (t == 1) return run_decode_fused(kv, layer, heads, q_dev, k_dev, v_dev, start, att_dev);
@@ -429,6 +439,7 @@ int wick_hip_kv_append_device(wick_hip_kv *kv, int layer, int start, int t, cons
     if (rc) return rc;
     if ((rc = check_span(kv, start, t))) return rc;
     if (!k_dev || !v_dev) return fail(WICK_HIP_EINVAL, "null k or v");
+    if ((rc = check_aligned(k_dev, "k_dev")) || (rc = check_aligned(v_dev, "v_dev"))) return rc;
     wick::AppendArgs a{k_dev, v_dev, kv->k_layer(layer), kv->v_layer(layer), kv->capacity, start, t, kv->kv_heads};
     hipError_t e = wick::launch_append(kv->head_dim, a, kv->stream);
     if (e != hipSuccess) return hip_fail(e, "append kernel launch");
@@ -479,6 +490,7 @@ int wick_hip_attention_device(wick_hip_kv *kv, int layer, int heads, const float
     if (rc) return rc;
     if ((rc = check_span(kv, start, t))) return rc;
     if (!q_dev || !att_dev) return fail(WICK_HIP_EINVAL, "null q or att");
+    if ((rc = check_aligned(q_dev, "q_dev")) || (rc = check_aligned(att_dev, "att_dev"))) return rc;
     return run_attention(kv, layer, heads, q_dev, t, start, att_dev);
 }
 
@@ -569,6 +581,9 @@ int wick_hip_attend_device(wick_hip_kv *kv, int layer, int heads, float *q_dev, 
     if (rc) return rc;
     if ((rc = check_span(kv, start, t))) return rc;
     if (!q_dev || !k_dev || !v_dev || !att_dev) return fail(WICK_HIP_EINVAL, "null q, k, v or att");
+    if ((rc = check_aligned(q_dev, "q_dev")) || (rc = check_aligned(k_dev, "k_dev")) ||
+        (rc = check_aligned(v_dev, "v_dev")) || (rc = check_aligned(att_dev, "att_dev")))
+        return rc;
     if (heads < 1 || heads % kv->kv_heads != 0)
         return fail(WICK_HIP_EINVAL, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv->kv_heads);
     if ((rc = run_prep(kv, layer, heads, q_dev, k_dev, v_dev, t, start))) return rc;

@@ -902,8 +902,9 @@ __device__ __forceinline__ void prefill_lean_body(const PrefillArgs &a) {
     using S = Shape<D>;
     static_assert(D == 64 || D == 128, "lean prefill: head_dim 64 or 128");
     constexpr int TG = S::TG;
-    __shared__ float sm_m[4][16], sm_l[4][16];
-    __shared__ float sm_o[4][16][D];
+    __shared__ float sm_m[4][16], sm_l[4][16], sm_e[4][16], sm_inv[16];
+    __shared__ int sm_row[16];
+    __shared__ __attribute__((aligned(16))) float sm_o[4][16][D];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kvh = blockIdx.x % a.kv_heads;
     const int idx = (int)(blockIdx.x / a.kv_heads), half = (a.nblocks + 1) >> 1;
@@ -960,23 +961,33 @@ __device__ __forceinline__ void prefill_lean_body(const PrefillArgs &a) {
 #pragma unroll
         for (int rr = 0; rr < 4; rr++) sm_o[w][col][out_dim<D>(g, rr, db)] = o[db][rr];
     __syncthreads();
-    // Merge the 4 waves' states (log2 units); wave 0 holds key 0, so M is finite.
-    for (int x = threadIdx.x; x < 16 * D; x += blockDim.x) {
-        const int cc = x / D, d = x % D;
-        const int rc = 16 * b + cc;
-        if (rc >= nrows) break;
+    // Merge the 4 waves' states (log2 units); wave 0 holds key 0, so M is
+    // finite.  The per-column weights, 1/sum and output row come first, once
+    // per column, so the per-element pass is 4 LDS float4 reads and FMAs.
+    if (threadIdx.x < 16) {
+        const int cc = threadIdx.x, rc = min(16 * b + cc, nrows - 1);
         float M = -INFINITY;
 #pragma unroll
         for (int ww = 0; ww < 4; ww++) M = fmaxf(M, sm_m[ww][cc]);
-        float oo = 0.f, L = 0.f;
+        float L = 0.f;
 #pragma unroll
         for (int ww = 0; ww < 4; ww++) {
             const float e = exp2_fast(sm_m[ww][cc] - M);
-            oo += sm_o[ww][cc][d] * e;
+            sm_e[ww][cc] = e;
             L += sm_l[ww][cc] * e;
         }
+        sm_inv[cc] = 1.0f / L;
         const int ic = rc / a.group, hc = rc % a.group;
-        a.att[(size_t)ic * heads * D + (size_t)(kvh * a.group + hc) * D + d] = oo / L;
+        sm_row[cc] = ic * heads + kvh * a.group + hc;
+    }
+    __syncthreads();
+    const int ncols = min(16, nrows - 16 * b);
+    for (int x = threadIdx.x; x < ncols * (D / 4); x += blockDim.x) {
+        const int cc = x / (D / 4), d = 4 * (x % (D / 4));
+        f4 acc = *reinterpret_cast<const f4 *>(&sm_o[0][cc][d]) * sm_e[0][cc];
+#pragma unroll
+        for (int ww = 1; ww < 4; ww++) acc += *reinterpret_cast<const f4 *>(&sm_o[ww][cc][d]) * sm_e[ww][cc];
+        *reinterpret_cast<f4 *>(a.att + (size_t)sm_row[cc] * D + d) = acc * sm_inv[cc];
     }
 }
 
