@@ -394,7 +394,8 @@ __device__ __forceinline__ void lean_load(__amdgpu_buffer_rsrc_t rk, __amdgpu_bu
     using S = Shape<D>;
 #pragma unroll
     for (int u = 0; u < S::TG; u++) {
-        const unsigned so = (unsigned)(p0 + 16 * u) * D * 4u;
+        // p0 is wave-uniform; saying so keeps the loads out of waterfall loops
+        const unsigned so = __builtin_amdgcn_readfirstlane((unsigned)(p0 + 16 * u) * D * 4u);
 #pragma unroll
         for (int j = 0; j < S::KJ; j++) t.k[u][j] = bload4(rk, vk + 64 * j, so);
 #pragma unroll
