@@ -398,6 +398,10 @@ __device__ __forceinline__ void lean_load(__amdgpu_buffer_rsrc_t rk, __amdgpu_bu
         const unsigned so = __builtin_amdgcn_readfirstlane((unsigned)(p0 + 16 * u) * D * 4u);
 #pragma unroll
         for (int j = 0; j < S::KJ; j++) t.k[u][j] = bload4(rk, vk + 64 * j, so);
+        // all of the tile's K loads go out before its first product (left to
+        // itself the scheduler issues them one or two at a time between the
+        // products, each a separate round trip)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int mm = 0; mm < 4; mm++)
 #pragma unroll
