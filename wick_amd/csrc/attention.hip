@@ -59,6 +59,16 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 // Lazy reference max of the lean core (log2 units): weights 2^(s - m) stay
 // below 2^8, so the running sums keep full f32 range and relative precision.
 constexpr float kLazyMax = 8.0f;
+// Starting reference max of the lazy core: finite, so 2^(s - m) needs no
+// guard (a masked score, -inf, still gives 0) and the first finite score of a
+// column replaces it.  A column that never sees a key keeps it, with l = 0.
+constexpr float kLazyFloor = -1e30f;
+
+// Max of two scores as gfx950's v_maximum3_f32: one instruction per 2-3 inputs,
+// where fmaxf first quiets each input that might be a signalling NaN (v_max x, x
+// per input).  It differs from fmaxf only for NaN inputs (propagated) and the
+// sign of a zero maximum, which exp2(s - m) does not see.
+__device__ __forceinline__ float smax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
 // max / sum over the four lanes that hold the same column (l, l^16, l^32, l^48).
 // v_permlane16_swap / v_permlane32_swap (gfx950) hand each lane the pair
@@ -67,11 +77,11 @@ constexpr float kLazyMax = 8.0f;
 // xor-shuffle step bit for bit.
 __device__ __forceinline__ float xor16_pair_max(float v) {
     const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    return smax(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 __device__ __forceinline__ float xor32_pair_max(float v) {
     const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    return smax(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 __device__ __forceinline__ float xor16_pair_sum(float v) {
     const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -447,8 +457,9 @@ __device__ __forceinline__ void lean_lane_offsets(int lane, unsigned &vk, unsign
 
 // One online-softmax step over a loaded group.  q is pre-scaled by
 // scale * log2(e), so scores and the reference max m are in log2 units; the
-// state (m, l, o) holds l = sum 2^(s - m), o = sum 2^(s - m) v, and m = -inf
-// until a column has seen a key.  LAZY: m moves (and l, o are rescaled) only
+// state (m, l, o) holds l = sum 2^(s - m), o = sum 2^(s - m) v.  Without
+// LAZY m is the running max, -inf until a column has seen a key.  LAZY: m
+// starts at kLazyFloor and moves (and l, o are rescaled) only
 // when a column's score exceeds it by more than kLazyMax, so the weights stay
 // below 2^kLazyMax and the rescale -- ~33 VALU instructions at head_dim 128,
 // which cost MFMA issue slots -- runs on few steps after the first (prefill:
@@ -479,19 +490,21 @@ __device__ __forceinline__ void lean_step(const LeanGroup<D> &t, const f4 (&q)[S
     }
     float lm = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < TG; u++) lm = fmaxf(lm, fmaxf(fmaxf(sc[u][0], sc[u][1]), fmaxf(sc[u][2], sc[u][3])));
+    for (int u = 0; u < TG; u++) lm = smax(lm, smax(smax(sc[u][0], sc[u][1]), smax(sc[u][2], sc[u][3])));
     const float cm = col_max(lm);
+    float mx;
     if constexpr (LAZY) {
-        const bool grow = cm > m + kLazyMax;  // false while both are -inf
+        const bool grow = cm > m + kLazyMax;  // never for cm = -inf
         if (__any(grow)) {
-            const float alpha = grow ? exp2_fast(m - cm) : 1.0f;  // 0 from m = -inf
+            const float alpha = grow ? exp2_fast(m - cm) : 1.0f;  // 0 from the floor
             l *= alpha;
 #pragma unroll
             for (int db = 0; db < S::DB; db++) o[db] *= alpha;
             m = grow ? cm : m;
         }
+        mx = m;
     } else {
-        const float mnew = fmaxf(m, cm);
+        const float mnew = smax(m, cm);
         const float alpha = exp2_fast(m - ((mnew == -INFINITY) ? 0.f : mnew));
         if (!__all(alpha == 1.0f)) {
             l *= alpha;
@@ -499,8 +512,8 @@ __device__ __forceinline__ void lean_step(const LeanGroup<D> &t, const f4 (&q)[S
             for (int db = 0; db < S::DB; db++) o[db] *= alpha;
         }
         m = mnew;
+        mx = (m == -INFINITY) ? 0.f : m;  // every score is -inf then
     }
-    const float mx = (m == -INFINITY) ? 0.f : m;  // every score is -inf then
     float ls = 0.f;
 #pragma unroll
     for (int u = 0; u < TG; u++)
@@ -981,7 +994,7 @@ __device__ __forceinline__ void prefill_lean_body(const PrefillArgs &a) {
     unsigned vk, vv;
     lean_lane_offsets<D>(lane, vk, vv);
 
-    float m = -INFINITY, l = 0.f;  // m in log2 units
+    float m = kLazyFloor, l = 0.f;  // m in log2 units
     f4 o[S::DB];
 #pragma unroll
     for (int db = 0; db < S::DB; db++) o[db] = f4{0.f, 0.f, 0.f, 0.f};
