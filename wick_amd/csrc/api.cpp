@@ -208,8 +208,11 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
     a.items = paired ? (a.nblocks + 1) / 2 : a.nblocks;
     a.split = kv->prefill_split;
     a.zigzag = (long long)a.kv_heads * a.nblocks <= (long long)kv->num_cus * kv->prefill_blocks_per_cu ? 1 : 0;
+    // A grid that takes more than one round: two row blocks per workgroup
+    // share each loaded tile (head_dim 128).
+    a.rows32 = a.zigzag ? 0 : 1;
     a.scale = scale;
-    kv->last_grid = wick::prefill_grid(a);
+    kv->last_grid = wick::prefill_grid(D, a);
     hipError_t e = wick::launch_prefill(D, a, kv->stream);
     if (e != hipSuccess) return hip_fail(e, "prefill kernel launch");
     return WICK_HIP_OK;

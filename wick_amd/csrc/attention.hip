@@ -953,76 +953,92 @@ constexpr long long lean_max_capacity() { return 0x7fffffffLL / (D * 4); }
 
 // head_dim 64 and 128.  One softmax step covers TG 16-key tiles (two at
 // head_dim 64, so that the step's fixed VALU work -- column max, rescale --
-// is spread over as many MFMAs as at head_dim 128).
-template <int D>
+// is spread over as many MFMAs as at head_dim 128).  RB consecutive 16-row
+// blocks per workgroup: with two, every loaded tile serves both blocks (half
+// the tile loads per product), at 2 waves per SIMD.
+template <int D, int RB>
 __device__ __forceinline__ void prefill_lean_body(const PrefillArgs &a) {
     using S = Shape<D>;
     static_assert(D == 64 || D == 128, "lean prefill: head_dim 64 or 128");
-    constexpr int TG = S::TG;
-    __shared__ float sm_m[4][16], sm_l[4][16], sm_e[4][16], sm_inv[16];
-    __shared__ int sm_row[16];
-    __shared__ __attribute__((aligned(16))) float sm_o[4][16][D];
+    static_assert(RB == 1 || RB == 2, "lean prefill: one or two row blocks");
+    constexpr int TG = S::TG, R = 16 * RB;  // rows per workgroup
+    __shared__ float sm_m[4][R], sm_l[4][R], sm_e[4][R], sm_inv[R];
+    __shared__ int sm_row[R];
+    __shared__ __attribute__((aligned(16))) float sm_o[4][R][D];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kvh = blockIdx.x % a.kv_heads;
-    const int idx = (int)(blockIdx.x / a.kv_heads), half = (a.nblocks + 1) >> 1;
-    const int b = (a.zigzag && idx >= half) ? idx - half : a.nblocks - 1 - idx;
+    const int nsb = (a.nblocks + RB - 1) / RB;
+    const int idx = (int)(blockIdx.x / a.kv_heads), half = (nsb + 1) >> 1;
+    const int sb = (a.zigzag && idx >= half) ? idx - half : nsb - 1 - idx;
     const float *Kh = a.k + (size_t)kvh * a.capacity * D;
     const float *Vh = a.v + (size_t)kvh * a.capacity * D;
     const int col = lane & 15, g = lane >> 4;
     const int heads = a.kv_heads * a.group;
     const int nrows = a.t * a.group;
-    const int r = 16 * b + col;
-    const bool valid = r < nrows;
-    const int i = valid ? r / a.group : 0, hh = valid ? r % a.group : 0;
-    const int imax = min(16 * b + 15, nrows - 1) / a.group;
-    const int kend = a.start + imax + 1;
-    const int lim = valid ? a.start + i + 1 : kend;           // padding rows see every key
-    const int lim_min = a.start + (16 * b) / a.group + 1;     // smallest limit in the block
+    const int kend = a.start + min(R * sb + R - 1, nrows - 1) / a.group + 1;
     const int nt = (kend + 15) >> 4;
     const int ks = 16 * ((w * nt) >> 2), ke = min(16 * (((w + 1) * nt) >> 2), kend);
 
     const float c = a.scale * kLog2e;
-    f4 q[S::KJ];
-    {
+    f4 q[RB][S::KJ];
+    int klimit[RB], unmasked_end[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+        const int r = R * sb + 16 * rb + col;
+        const bool valid = r < nrows;
+        const int i = valid ? r / a.group : 0, hh = valid ? r % a.group : 0;
+        const int lim = valid ? a.start + i + 1 : kend;  // padding rows see every key
+        // smallest limit in the block (a block wholly past the rows: its first row's)
+        const int lim_min = a.start + min(R * sb + 16 * rb, nrows - 1) / a.group + 1;
+        klimit[rb] = min(lim, ke);
+        unmasked_end[rb] = min(lim_min, ke);
         const float *row = valid ? a.q + (size_t)i * heads * D + (size_t)(kvh * a.group + hh) * D : a.q;
         const float keep = valid ? c : 0.f;
 #pragma unroll
-        for (int j = 0; j < S::KJ; j++) q[j] = *reinterpret_cast<const f4 *>(row + 16 * j + 4 * g) * keep;
+        for (int j = 0; j < S::KJ; j++) q[rb][j] = *reinterpret_cast<const f4 *>(row + 16 * j + 4 * g) * keep;
     }
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(Kh, (unsigned)kend * D * 4u);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vh, (unsigned)kend * D * 4u);
     unsigned vk, vv;
     lean_lane_offsets<D>(lane, vk, vv);
 
-    float m = kLazyFloor, l = 0.f;  // m in log2 units
-    f4 o[S::DB];
+    float m[RB], l[RB];  // m in log2 units
+    f4 o[RB][S::DB];
 #pragma unroll
-    for (int db = 0; db < S::DB; db++) o[db] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int rb = 0; rb < RB; rb++) {
+        m[rb] = kLazyFloor;
+        l[rb] = 0.f;
+#pragma unroll
+        for (int db = 0; db < S::DB; db++) o[rb][db] = f4{0.f, 0.f, 0.f, 0.f};
+    }
     const int nsteps = (ke - ks + 16 * TG - 1) / (16 * TG);
-    const int unmasked_end = min(lim_min, ke);
-    const int klimit = min(lim, ke);
     for (int n = 0; n < nsteps; n++) {
         const int p0 = ks + 16 * TG * n;
         LeanGroup<D> t;
         lean_load<D>(rk, rv, vk, vv, p0, t);
-        // keys past this row's causal limit or past the wave's range
-        lean_step<D, true>(t, q, p0, p0 + 16 * TG > unmasked_end, klimit, g, m, l, o);
-    }
-    l = col_sum(l);
-    if (g == 0) {
-        sm_m[w][col] = m;
-        sm_l[w][col] = l;
+        // keys past a row's causal limit or past the wave's range
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+            lean_step<D, true>(t, q[rb], p0, p0 + 16 * TG > unmasked_end[rb], klimit[rb], g, m[rb], l[rb], o[rb]);
     }
 #pragma unroll
-    for (int db = 0; db < S::DB; db++)
+    for (int rb = 0; rb < RB; rb++) {
+        const float ls = col_sum(l[rb]);
+        if (g == 0) {
+            sm_m[w][16 * rb + col] = m[rb];
+            sm_l[w][16 * rb + col] = ls;
+        }
 #pragma unroll
-        for (int rr = 0; rr < 4; rr++) sm_o[w][col][out_dim<D>(g, rr, db)] = o[db][rr];
+        for (int db = 0; db < S::DB; db++)
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++) sm_o[w][16 * rb + col][out_dim<D>(g, rr, db)] = o[rb][db][rr];
+    }
     __syncthreads();
     // Merge the 4 waves' states (log2 units); wave 0 holds key 0, so M is
     // finite.  The per-column weights, 1/sum and output row come first, once
     // per column, so the per-element pass is 4 LDS float4 reads and FMAs.
-    if (threadIdx.x < 16) {
-        const int cc = threadIdx.x, rc = min(16 * b + cc, nrows - 1);
+    if (threadIdx.x < R) {
+        const int cc = threadIdx.x, rc = min(R * sb + cc, nrows - 1);
         float M = -INFINITY;
 #pragma unroll
         for (int ww = 0; ww < 4; ww++) M = fmaxf(M, sm_m[ww][cc]);
@@ -1038,7 +1054,7 @@ __device__ __forceinline__ void prefill_lean_body(const PrefillArgs &a) {
         sm_row[cc] = ic * heads + kvh * a.group + hc;
     }
     __syncthreads();
-    const int ncols = min(16, nrows - 16 * b);
+    const int ncols = min(R, nrows - R * sb);
     for (int x = threadIdx.x; x < ncols * (D / 4); x += blockDim.x) {
         const int cc = x / (D / 4), d = 4 * (x % (D / 4));
         f4 acc = *reinterpret_cast<const f4 *>(&sm_o[0][cc][d]) * sm_e[0][cc];
@@ -1050,7 +1066,15 @@ __device__ __forceinline__ void prefill_lean_body(const PrefillArgs &a) {
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prefill_lean_kernel_d128(
     const PrefillArgs a) {
-    prefill_lean_body<128>(a);
+    prefill_lean_body<128, 1>(a);
+}
+
+// Two row blocks per workgroup (234 VGPRs, 2 waves per SIMD), for grids that
+// are not resident at once: config 3 T=2048 188.6 -> 175.9 us.  A grid that is
+// resident at once keeps one block per workgroup (T=512: 17.9 against 24.4 us).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void prefill_lean2_kernel_d128(
+    const PrefillArgs a) {
+    prefill_lean_body<128, 2>(a);
 }
 
 // head_dim 64 held to 4 waves per SIMD (120 VGPRs, no spills; left to
@@ -1058,7 +1082,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
 // against 89.5-91 us)
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prefill_lean_kernel_d64(
     const PrefillArgs a) {
-    prefill_lean_body<64>(a);
+    prefill_lean_body<64, 1>(a);
 }
 
 // ------------------------------------------------------------------ append
@@ -1168,13 +1192,21 @@ int prefill_blocks_per_cu(int head_dim) {
     return (e == hipSuccess && n > 0) ? n : 1;
 }
 
-int prefill_grid(const PrefillArgs &a) {
+// The lean head_dim-128 kernel with two row blocks per workgroup.
+static bool prefill_uses_rows32(int head_dim, const PrefillArgs &a) {
+    return a.split && a.rows32 && head_dim == 128 && a.capacity <= lean_max_capacity<128>();
+}
+
+int prefill_grid(int head_dim, const PrefillArgs &a) {
+    if (prefill_uses_rows32(head_dim, a)) return a.kv_heads * ((a.nblocks + 1) / 2);
     return a.split ? a.kv_heads * a.nblocks : a.kv_heads * ((a.items + 3) / 4);
 }
 
 hipError_t launch_prefill(int head_dim, const PrefillArgs &a, hipStream_t s) {
-    const int grid = prefill_grid(a);
-    if (a.split && head_dim == 128 && a.capacity <= lean_max_capacity<128>()) {
+    const int grid = prefill_grid(head_dim, a);
+    if (prefill_uses_rows32(head_dim, a)) {
+        hipLaunchKernelGGL(prefill_lean2_kernel_d128, dim3(grid), dim3(256), 0, s, a);
+    } else if (a.split && head_dim == 128 && a.capacity <= lean_max_capacity<128>()) {
         hipLaunchKernelGGL(prefill_lean_kernel_d128, dim3(grid), dim3(256), 0, s, a);
     } else if (a.split && head_dim == 64 && a.capacity <= lean_max_capacity<64>()) {
         hipLaunchKernelGGL(prefill_lean_kernel_d64, dim3(grid), dim3(256), 0, s, a);

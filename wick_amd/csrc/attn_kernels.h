@@ -43,6 +43,7 @@ struct PrefillArgs {
     int capacity, t, start, kv_heads, group, nblocks, items, paired;
     int split;        // 1: prefill_split_kernel (4-way key split per workgroup)
     int zigzag;       // split kernel: the grid is resident at once; pair heavy and light blocks
+    int rows32;       // lean head_dim-128 kernel: two 16-row blocks per workgroup (set when zigzag is not)
     float scale;
 };
 
@@ -73,7 +74,7 @@ int prefill_blocks_per_cu(int head_dim);
 
 // Launches decode_kernel and, when it splits the keys, decode_merge_kernel.
 hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_t s);
-int prefill_grid(const PrefillArgs &a);
+int prefill_grid(int head_dim, const PrefillArgs &a);
 hipError_t launch_prefill(int head_dim, const PrefillArgs &a, hipStream_t s);
 hipError_t launch_append(int head_dim, const AppendArgs &a, hipStream_t s);
 // prep.hip: bias, QK-norm, RoPE of q and k; k and v appended to the cache.
