@@ -193,20 +193,23 @@ def test_prefill_schedules_agree_within_tolerance(split, d):
     check(q, k, v, t, start, 8, 2, d, options=[(_native.OPT_PREFILL_SPLIT, split)])
 
 
-@pytest.mark.parametrize("t,start,heads,kv_heads", [(1000, 37, 16, 8), (500, 0, 32, 8), (777, 300, 24, 8)])
-def test_prefill_two_blocks_per_workgroup(t, start, heads, kv_heads):
-    # Grids of more than one round: the head_dim-128 kernel gives each workgroup two
-    # 16-row blocks (odd block counts leave the last pair half empty).
-    q, k, v = make_inputs(t + start + heads, t, start, heads, kv_heads, 128)
+@pytest.mark.parametrize("t,start,heads,kv_heads,d", [(1032, 37, 16, 8, 128), (516, 0, 32, 8, 128),
+                                                      (777, 300, 24, 8, 128), (600, 200, 32, 4, 64),
+                                                      (2050, 0, 9, 3, 64)])
+def test_prefill_two_blocks_per_workgroup(t, start, heads, kv_heads, d):
+    # Grids that still give each of the 256 CUs two workgroups with two 16-row blocks
+    # per workgroup take that kernel (odd block counts leave the last pair half empty;
+    # the head_dim-64 shapes are also resident at once, so heavy and light pairs mix).
+    q, k, v = make_inputs(t + start + heads, t, start, heads, kv_heads, d)
     L = start + t
-    with DeviceKvCache(1, L, kv_heads, 128) as kv:
+    with DeviceKvCache(1, L, kv_heads, d) as kv:
         kv.append(0, 0, k, v)
         got = kv.attention(0, heads, q, start)
         nblocks = (t * (heads // kv_heads) + 15) // 16
         assert kv.last_grid() == kv_heads * ((nblocks + 1) // 2), "two blocks per workgroup expected"
         again = kv.attention(0, heads, q, start)
     assert np.array_equal(got, again)
-    want = ol.attention(q, k, v, t, start, heads, kv_heads, 128)
+    want = ol.attention(q, k, v, t, start, heads, kv_heads, d)
     ok, mabs, mrel = within_tol(got, want)
     print(f"t={t} start={start} Hq={heads} Hkv={kv_heads}: max abs {mabs:.2e} max rel {mrel:.2e}")
     assert ok, f"max abs {mabs:.3e}, max rel {mrel:.3e}"

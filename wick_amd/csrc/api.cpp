@@ -59,7 +59,7 @@ struct wick_hip_kv {
     int ws_units = 0;
     // options
     int decode_chunk = 0, pairing = -1, prefill_split = 1, last_grid = 0;
-    int decode_blocks_per_cu = 1, prefill_blocks_per_cu = 1;
+    int decode_blocks_per_cu = 1, prefill_blocks_per_cu = 1, prefill2_blocks_per_cu = 1;
     // input preparation (wick_hip_kv_set_rope / wick_hip_kv_set_prep)
     float *rope_cos = nullptr, *rope_sin = nullptr;  // [capacity][head_dim/2]
     struct LayerPrep {
@@ -207,10 +207,15 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
     a.paired = paired;
     a.items = paired ? (a.nblocks + 1) / 2 : a.nblocks;
     a.split = kv->prefill_split;
-    a.zigzag = (long long)a.kv_heads * a.nblocks <= (long long)kv->num_cus * kv->prefill_blocks_per_cu ? 1 : 0;
-    // A grid that takes more than one round: two row blocks per workgroup
-    // share each loaded tile (head_dim 128).
-    a.rows32 = a.zigzag ? 0 : 1;
+    // Two row blocks per workgroup share each loaded tile, where that grid
+    // still gives every CU two workgroups; zigzag pairing where the launched
+    // grid is resident at once.
+    const long long grid1 = (long long)a.kv_heads * a.nblocks, grid2 = (long long)a.kv_heads * ((a.nblocks + 1) / 2);
+    a.rows32 = wick::prefill_has_rows32(D, kv->capacity, a.split) && grid2 >= 2LL * kv->num_cus ? 1 : 0;
+    a.zigzag = (a.rows32 ? grid2 : grid1) <=
+                       (long long)kv->num_cus * (a.rows32 ? kv->prefill2_blocks_per_cu : kv->prefill_blocks_per_cu)
+                   ? 1
+                   : 0;
     a.scale = scale;
     kv->last_grid = wick::prefill_grid(D, a);
     hipError_t e = wick::launch_prefill(D, a, kv->stream);
@@ -370,7 +375,8 @@ int wick_hip_kv_create(int layers, int capacity, int kv_heads, int head_dim, wic
         kv->num_cus = prop.multiProcessorCount;
         kv->prep.resize(layers);
         kv->decode_blocks_per_cu = wick::decode_blocks_per_cu(head_dim);
-        kv->prefill_blocks_per_cu = wick::prefill_blocks_per_cu(head_dim);
+        kv->prefill_blocks_per_cu = wick::prefill_blocks_per_cu(head_dim, 0);
+        kv->prefill2_blocks_per_cu = wick::prefill_blocks_per_cu(head_dim, 1);
         if ((e = hipStreamCreateWithFlags(&kv->own_stream, hipStreamNonBlocking)) != hipSuccess) { rc = hip_fail(e, "hipStreamCreate"); break; }
         kv->stream = kv->own_stream;
         const size_t bytes = (size_t)layers * kv->layer_floats() * sizeof(float);

@@ -1070,8 +1070,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
 }
 
 // Two row blocks per workgroup (234 VGPRs, 2 waves per SIMD), for grids that
-// are not resident at once: config 3 T=2048 188.6 -> 175.9 us.  A grid that is
-// resident at once keeps one block per workgroup (T=512: 17.9 against 24.4 us).
+// still give every CU two workgroups: config 3 T=2048 188.6 -> 175.9 us.  With
+// fewer (T=512: one per CU) one block per workgroup is faster, 17.9 against
+// 24.4 us.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void prefill_lean2_kernel_d128(
     const PrefillArgs a) {
     prefill_lean_body<128, 2>(a);
@@ -1083,6 +1084,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prefill_lean_kernel_d64(
     const PrefillArgs a) {
     prefill_lean_body<64, 1>(a);
+}
+
+// Two row blocks per workgroup at head_dim 64 (168 VGPRs, 3 waves per SIMD):
+// config 4 82.5 -> 76.8 us per layer.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void prefill_lean2_kernel_d64(
+    const PrefillArgs a) {
+    prefill_lean_body<64, 2>(a);
 }
 
 // ------------------------------------------------------------------ append
@@ -1179,22 +1187,35 @@ hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_
     return hipGetLastError();
 }
 
-int prefill_blocks_per_cu(int head_dim) {
+int prefill_blocks_per_cu(int head_dim, int rows32) {
     int n = 0;
     hipError_t e = hipErrorInvalidValue;
     switch (head_dim) {
     case 16: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_split_kernel<16>, 256, 0); break;
     case 32: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_split_kernel<32>, 256, 0); break;
-    case 64: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_lean_kernel_d64, 256, 0); break;
-    case 128: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_lean_kernel_d128, 256, 0); break;
+    case 64:
+        e = rows32 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_lean2_kernel_d64, 256, 0)
+                   : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_lean_kernel_d64, 256, 0);
+        break;
+    case 128:
+        e = rows32 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_lean2_kernel_d128, 256, 0)
+                   : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_lean_kernel_d128, 256, 0);
+        break;
     default: break;
     }
     return (e == hipSuccess && n > 0) ? n : 1;
 }
 
-// The lean head_dim-128 kernel with two row blocks per workgroup.
+bool prefill_has_rows32(int head_dim, int capacity, int split) {
+    if (!split) return false;
+    if (head_dim == 128) return capacity <= lean_max_capacity<128>();
+    if (head_dim == 64) return capacity <= lean_max_capacity<64>();
+    return false;
+}
+
+// A lean kernel with two row blocks per workgroup.
 static bool prefill_uses_rows32(int head_dim, const PrefillArgs &a) {
-    return a.split && a.rows32 && head_dim == 128 && a.capacity <= lean_max_capacity<128>();
+    return a.rows32 && prefill_has_rows32(head_dim, a.capacity, a.split);
 }
 
 int prefill_grid(int head_dim, const PrefillArgs &a) {
@@ -1204,8 +1225,10 @@ int prefill_grid(int head_dim, const PrefillArgs &a) {
 
 hipError_t launch_prefill(int head_dim, const PrefillArgs &a, hipStream_t s) {
     const int grid = prefill_grid(head_dim, a);
-    if (prefill_uses_rows32(head_dim, a)) {
+    if (prefill_uses_rows32(head_dim, a) && head_dim == 128) {
         hipLaunchKernelGGL(prefill_lean2_kernel_d128, dim3(grid), dim3(256), 0, s, a);
+    } else if (prefill_uses_rows32(head_dim, a)) {
+        hipLaunchKernelGGL(prefill_lean2_kernel_d64, dim3(grid), dim3(256), 0, s, a);
     } else if (a.split && head_dim == 128 && a.capacity <= lean_max_capacity<128>()) {
         hipLaunchKernelGGL(prefill_lean_kernel_d128, dim3(grid), dim3(256), 0, s, a);
     } else if (a.split && head_dim == 64 && a.capacity <= lean_max_capacity<64>()) {

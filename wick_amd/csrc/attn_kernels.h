@@ -43,7 +43,7 @@ struct PrefillArgs {
     int capacity, t, start, kv_heads, group, nblocks, items, paired;
     int split;        // 1: prefill_split_kernel (4-way key split per workgroup)
     int zigzag;       // split kernel: the grid is resident at once; pair heavy and light blocks
-    int rows32;       // lean head_dim-128 kernel: two 16-row blocks per workgroup (set when zigzag is not)
+    int rows32;       // lean kernels: two 16-row blocks per workgroup
     float scale;
 };
 
@@ -70,7 +70,9 @@ size_t decode_workspace_floats(int units, int head_dim);
 // Decode workgroups one CU holds at once (from the kernel's register and LDS use).
 int decode_blocks_per_cu(int head_dim);
 // The same for the split prefill kernel.
-int prefill_blocks_per_cu(int head_dim);
+int prefill_blocks_per_cu(int head_dim, int rows32);
+// Whether the prefill kernel for this shape can take two row blocks per workgroup.
+bool prefill_has_rows32(int head_dim, int capacity, int split);
 
 // Launches decode_kernel and, when it splits the keys, decode_merge_kernel.
 hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_t s);
