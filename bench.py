@@ -470,7 +470,7 @@ def main():
         us2048, fl2048 = pre[2048]
         tf = fl2048 / (us2048 * 1e-6) / 1e12
         out["prefill_tflops"] = round(tf, 2)
-        out["roofline_prefill"] = {"bound": "mfma", "kernel": "wick::prefill_lean_kernel_d128",
+        out["roofline_prefill"] = {"bound": "mfma", "kernel": "wick::prefill_lean2_kernel_d128",
                                    "achieved": round(tf, 2), "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                                    "frac": round(tf / F32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
                                    "flops_per_launch": fl2048, "us_per_launch": round(us2048, 2),
