@@ -8,8 +8,9 @@
 //
 // All kernels share one wave-level layout: a wave owns 16 "columns" -- 16
 // query heads of one kv head (decode) or 16 flattened (token, head) rows of
-// one kv head (prefill) -- and streams 16-key tiles of K and V through two f32
-// MFMAs (the lean core lean_load/lean_step at head_dim 64 and 128, the older
+// one kv head (prefill; the two-block prefill kernels run two such sets of
+// columns against every tile) -- and streams 16-key tiles of K and V through
+// two f32 MFMAs (the lean core lean_load/lean_step at head_dim 64 and 128, the older
 // attend_range core at head_dim 16 and 32):
 //   S^T[16 keys x 16 cols] = K_tile[16 x D] . Q^T[D x 16]       (v_mfma_f32_16x16x4_f32)
 //   O^T[D x 16 cols]      += V_tile^T[D x 16] . P^T[16 x 16]     (same instruction)
@@ -943,9 +944,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void p
 // ------------------------------------------------------------------ lean prefill
 //
 // The split kernel above spends ~113 VALU instructions per 16-key tile on 64
-// MFMAs at head_dim 128.  The lean variant keeps its work split (16-row
-// block per workgroup, keys split over the 4 waves, heaviest blocks first)
-// and runs each tile through lean_load / lean_step (~30 VALU per tile).
+// MFMAs at head_dim 128.  The lean variant keeps its work split (one or two
+// 16-row blocks per workgroup, keys split over the 4 waves, heaviest blocks
+// first) and runs each tile through lean_load / lean_step (~30 VALU per tile).
+//
 // Largest cache capacity the lean kernel addresses with 32-bit buffer offsets
 // (bytes of one kv head's rows must fit a signed 32-bit range).
 template <int D>
