@@ -78,7 +78,9 @@ int wick_hip_model_prefill(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *p
 /* The greedy loop of cmd_bench: `steps` single-token forwards starting with
  * token `first` at position `start`; after forward i the argmax becomes
  * out[i] and the input of forward i+1.  Ids stay on the device between
- * steps; the call returns when out [steps] (host) is filled. */
+ * steps; runs of steps that share a decode launch plan replay one captured
+ * step as a HIP graph (same results as launching each step).  The call
+ * returns when out [steps] (host) is filled. */
 int wick_hip_model_decode(wick_hip_model *m, wick_hip_kv *kv, uint32_t first, int start, int steps, uint32_t *out);
 
 /* Sampler::new (src/sampler.rs:67-71) for this model's vocabulary, launching

@@ -102,27 +102,34 @@ def test_smollm2_135m_greedy_ids_match_cpu():
 
 
 def test_decode_matches_step_by_step_forward():
-    """decode() keeps ids on the device; forward() + host argmax must give the same chain."""
+    """decode() keeps ids on the device and replays runs of steps that share a decode plan
+    from a captured HIP graph; forward() + host argmax, launched step by step, must give
+    the same chain and the same cache bits.  40 -> 240 positions: one-chunk plans of 64,
+    128 and 192 keys, then split-K with the merge pass (runs of 24, 64, 64 and 48 steps)."""
     cfg = smollm2_135m()
     cfg.layers = 4
     w = random_weights(cfg, seed=3)
     prompt = random_prompt(4, 40, cfg.vocab)
+    n = 200
     with DeviceModel(cfg, w) as m:
-        c1 = m.new_cache(80)
+        c1 = m.new_cache(256)
         first = m.prefill(c1, prompt)
-        chain = m.decode(c1, first, 20)
-        c2 = m.new_cache(80)
+        chain = m.decode(c1, first, n)
+        c2 = m.new_cache(256)
         logits = m.forward(c2, prompt)
         assert int(np.argmax(logits[0])) == first
         tok, steps = first, []
-        for _ in range(20):
+        for _ in range(n):
             logits = m.forward(c2, [tok])
             tok = ol.argmax(logits[0])
             steps.append(tok)
-        k1, v1 = c1.read(3, 0, 60)
-        k2, v2 = c2.read(3, 0, 60)
+        k1, v1 = c1.read(3, 0, 40 + n)
+        k2, v2 = c2.read(3, 0, 40 + n)
+        c1.len = 40  # prefix reuse: back to the prompt, one step launched directly
+        again = m.decode(c1, first, 1)
     assert chain == steps
     assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+    assert again == chain[:1]
 
 
 def test_prefill_chunks_of_256():

@@ -128,14 +128,9 @@ int check_span(const wick_hip_kv *kv, int start, int t) {
     return WICK_HIP_OK;
 }
 
-// Split-K schedule of one decode call over len positions: fills the shape
-// fields of *a and kv->last_grid.
-int plan_decode(wick_hip_kv *kv, int layer, int group, int len, const float *q_dev, float *att_dev,
-                wick::DecodeArgs *a) {
-    const int hslices = (group + wick::kTileRows - 1) / wick::kTileRows;
-    const int units = kv->kv_heads * hslices;
-    int rc = ensure_workspace(kv, units);
-    if (rc) return rc;
+// Chunk size and count of a decode call over len positions for `units`
+// (kv head x 16-head slice) workgroup rows.
+void plan_chunks(const wick_hip_kv *kv, int units, int len, int *chunk_out, int *nchunks_out) {
     int chunk = kv->decode_chunk;
     if (chunk <= 0 && len <= wick::kDecodeSingleChunkMax) {
         // Short context: one workgroup per unit and no merge pass.  Its
@@ -152,7 +147,20 @@ int plan_decode(wick_hip_kv *kv, int layer, int group, int len, const float *q_d
     chunk = std::max(64, (chunk + 63) / 64 * 64);
     const int min_chunk = (len + wick::kDecodeMaxChunks - 1) / wick::kDecodeMaxChunks;
     if (chunk < min_chunk) chunk = (min_chunk + 63) / 64 * 64;
-    const int nchunks = (len + chunk - 1) / chunk;
+    *chunk_out = chunk;
+    *nchunks_out = (len + chunk - 1) / chunk;
+}
+
+// Split-K schedule of one decode call over len positions: fills the shape
+// fields of *a and kv->last_grid.
+int plan_decode(wick_hip_kv *kv, int layer, int group, int len, const float *q_dev, float *att_dev,
+                wick::DecodeArgs *a) {
+    const int hslices = (group + wick::kTileRows - 1) / wick::kTileRows;
+    const int units = kv->kv_heads * hslices;
+    int rc = ensure_workspace(kv, units);
+    if (rc) return rc;
+    int chunk, nchunks;
+    plan_chunks(kv, units, len, &chunk, &nchunks);
     a->q = q_dev;
     a->k = kv->k_layer(layer);
     a->v = kv->v_layer(layer);
@@ -284,7 +292,7 @@ int run_prep(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k
 // One token: the preparation fused into the decode kernel's prologue (q from
 // the raw projections, k and v appended at position start), then attention.
 int run_decode_fused(wick_hip_kv *kv, int layer, int heads, const float *q_raw, const float *k_raw,
-                     const float *v_raw, int start, float *att_dev) {
+                     const float *v_raw, int start, float *att_dev, const int *len_dev) {
     PrepConsts c;
     int rc = prep_consts(kv, layer, heads, &c);
     if (rc) return rc;
@@ -302,6 +310,7 @@ int run_decode_fused(wick_hip_kv *kv, int layer, int heads, const float *q_raw, 
     a.rope_cos = kv->rope_cos;
     a.rope_sin = kv->rope_sin;
     a.eps = c.eps;
+    a.len_dev = len_dev;
     hipError_t e = wick::launch_decode(kv->head_dim, a, kv->last_grid, kv->stream);
     if (e != hipSuccess) return hip_fail(e, "decode kernel launch");
     return WICK_HIP_OK;
@@ -322,7 +331,7 @@ int set_error(int code, const char *fmt, ...) {
 }
 
 int attend_model(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev, const float *v_dev, int t,
-                 int start, float *att_dev) {
+                 int start, float *att_dev, const int *len_dev) {
     int rc = check_kv(kv, layer);
     if (rc) return rc;
     if ((rc = check_span(kv, start, t))) return rc;
@@ -332,9 +341,18 @@ int attend_model(wick_hip_kv *kv, int layer, int heads, float *q_dev, const floa
         return rc;
     if (heads < 1 || heads % kv->kv_heads != 0)
         return fail(WICK_HIP_EINVAL, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv->kv_heads);
-    if (t == 1) return run_decode_fused(kv, layer, heads, q_dev, k_dev, v_dev, start, att_dev);
+    if (t == 1) return run_decode_fused(kv, layer, heads, q_dev, k_dev, v_dev, start, att_dev, len_dev);
+    if (len_dev) return fail(WICK_HIP_EINVAL, "a device cache length needs t = 1");
     if ((rc = run_prep(kv, layer, heads, q_dev, k_dev, v_dev, t, start))) return rc;
     return run_attention(kv, layer, heads, q_dev, t, start, att_dev);
+}
+
+long long decode_plan_key(const wick_hip_kv *kv, int heads, int len) {
+    const int group = heads / kv->kv_heads;
+    const int hslices = (group + wick::kTileRows - 1) / wick::kTileRows;
+    int chunk, nchunks;
+    plan_chunks(kv, kv->kv_heads * hslices, len, &chunk, &nchunks);
+    return ((long long)chunk << 32) | (unsigned)nchunks;
 }
 
 bool kv_info(const wick_hip_kv *kv, KvInfo *out) {

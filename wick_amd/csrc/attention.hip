@@ -585,7 +585,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
     const int head0 = kvh * a.group + col0;
     const float *Kh = a.k + (size_t)kvh * a.capacity * D;
     const float *Vh = a.v + (size_t)kvh * a.capacity * D;
-    const int kbeg = chunk * a.chunk, kend = min(kbeg + a.chunk, a.len);
+    // the cache length: the argument, or (graph-replayed decode loop) a device counter
+    const int len = a.len_dev ? *a.len_dev : a.len;
+    const int kbeg = chunk * a.chunk, kend = min(kbeg + a.chunk, len);
 
     const int col = lane & 15, g = lane >> 4;
     f4 q[S::KJ];
@@ -595,7 +597,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
         // k and v rows of the kv head (to the cache).  Workgroups of other
         // head slices of the same kv head write the same bits there.  The
         // barrier orders those stores before this workgroup's tile loads.
-        const int pos = a.len - 1;
+        const int pos = len - 1;
         const bool last = chunk == a.nchunks - 1;
         const int nrows = ncols + (last ? 2 : 0);
         const float *cr = a.rope_cos + (size_t)pos * (D / 2), *sr = a.rope_sin + (size_t)pos * (D / 2);
@@ -655,7 +657,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
         }
     } else {
         init_state<D>(st);
-        attend_range<D, PP>(Kh, Vh, kbeg, kend, w * S::TG, NW * S::TG, a.len, a.scale, q, lane, st);
+        attend_range<D, PP>(Kh, Vh, kbeg, kend, w * S::TG, NW * S::TG, len, a.scale, q, lane, st);
         st.m *= kLog2e;  // the merges take maxima in log2 units
     }
     st.l = col_sum(st.l);

@@ -33,6 +33,10 @@ struct DecodeArgs {
     const float *bq, *bk, *bv, *qn, *kn;
     const float *rope_cos, *rope_sin;  // [capacity][D/2] tables
     float eps;
+    // When non-null the kernels read the cache length here instead of len (a
+    // HIP graph replays one decode step for successive lengths); chunk and
+    // nchunks must then suit every length it takes: plan_decode's plan for it.
+    const int *len_dev;
 };
 
 struct PrefillArgs {
@@ -92,8 +96,15 @@ bool kv_info(const wick_hip_kv *kv, KvInfo *out);
 // src/model.rs:464-485 for one layer on device arrays, as wick_hip_attend_device
 // except that q_dev is scratch (its contents afterwards are unspecified): for
 // one token the preparation runs in the decode kernel's prologue.
+// len_dev (t = 1 only): the decode kernels read the cache length there (a
+// captured step replayed for successive positions); start still chooses the
+// launch plan, which decode_plan_key identifies.
 int attend_model(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev, const float *v_dev, int t,
-                 int start, float *att_dev);
+                 int start, float *att_dev, const int *len_dev = nullptr);
+
+// The decode launch plan (chunk size and count) for `heads` query heads over
+// len cached positions: equal keys launch the same kernels on the same grids.
+long long decode_plan_key(const wick_hip_kv *kv, int heads, int len);
 
 // Record the message wick_hip_last_error() returns on this thread; returns code.
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));

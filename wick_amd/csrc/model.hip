@@ -277,10 +277,12 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
     for (int c = threadIdx.x; c < n; c += 256) o[c] = xr[c] * scale * g[c];
 }
 
+// step (graph-replayed decode loop): the token is tokens[*step + i].
 __global__ __launch_bounds__(256) void embed_kernel(const float *__restrict__ embed, const uint32_t *__restrict__ tokens,
-                                                    float *__restrict__ x, int hidden) {
+                                                    const int *__restrict__ step, float *__restrict__ x, int hidden) {
     const int i = blockIdx.x;
-    const f4 *src = reinterpret_cast<const f4 *>(embed + (size_t)tokens[i] * hidden);
+    const int at = (step ? *step : 0) + i;
+    const f4 *src = reinterpret_cast<const f4 *>(embed + (size_t)tokens[at] * hidden);
     f4 *dst = reinterpret_cast<f4 *>(x + (size_t)i * hidden);
     for (int c = threadIdx.x; c < hidden / 4; c += blockDim.x) dst[c] = src[c];
 }
@@ -298,7 +300,10 @@ __device__ __forceinline__ void arg_better(float v, int i, float &bv, int &bi) {
     }
 }
 
-__global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ x, int n, uint32_t *__restrict__ out) {
+// step, len (graph-replayed decode loop): the id goes to out[*step + 1], then
+// *step and *len advance to the next forward's token and cache length.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ x, int n, uint32_t *__restrict__ out,
+                                                      int *__restrict__ step, int *__restrict__ len) {
     constexpr int U = 8;
     __shared__ float sv[16];
     __shared__ int si[16];
@@ -341,7 +346,14 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
         for (int k = 1; k < 16; k++) arg_better(sv[k], si[k], bv, bi);
         // all values NaN (bi unset) or x[0] NaN: wick keeps index 0
         if (bi == 0x7fffffff || isnan(x[0])) bi = 0;
-        *out = (uint32_t)bi;
+        if (step) {
+            const int k = *step;
+            out[k + 1] = (uint32_t)bi;
+            *step = k + 1;
+            *len += 1;
+        } else {
+            *out = (uint32_t)bi;
+        }
     }
 }
 
@@ -404,14 +416,25 @@ hipError_t launch_rmsnorm(const float *x, const float *g, float eps, float *out,
     return hipGetLastError();
 }
 
-hipError_t launch_embed(const float *embed, const uint32_t *tokens, float *x, int t, int hidden, hipStream_t s) {
+hipError_t launch_embed(const float *embed, const uint32_t *tokens, float *x, int t, int hidden, hipStream_t s,
+                        const int *step) {
     if (t <= 0) return hipSuccess;
-    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)t), dim3(256), 0, s, embed, tokens, x, hidden);
+    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)t), dim3(256), 0, s, embed, tokens, step, x, hidden);
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float *x, int n, uint32_t *out, hipStream_t s) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, x, n, out);
+__global__ void set_step_kernel(int *counters, int step, int len) {
+    counters[0] = step;
+    counters[1] = len;
+}
+
+hipError_t launch_set_step(int *counters, int step, int len, hipStream_t s) {
+    hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, counters, step, len);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float *x, int n, uint32_t *out, hipStream_t s, int *step, int *len) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, x, n, out, step, len);
     return hipGetLastError();
 }
 

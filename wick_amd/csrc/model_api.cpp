@@ -75,6 +75,7 @@ struct wick_hip_model {
     int cap_ids = 0;
     uint32_t *ids = nullptr;  // token ids on the device (prompt, or the greedy chain)
     uint32_t *pinned_id = nullptr;  // page-locked slot the generate loop reads ids through
+    int *counters = nullptr;        // [step, cache length] read by a replayed decode step
 };
 
 namespace {
@@ -182,12 +183,16 @@ int product(wick_hip_model *m, int epi, wick::GemvArgs g, const char *what) {
 
 // Model::forward for t tokens whose ids are on the device; logits of the last
 // token (or of all t when all_logits) go to m->logits.  Queued on m->stream.
-int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, int t, int start, bool all_logits) {
+// With counters (t = 1, a step captured for replay) the token is
+// tok_dev[counters[0]] and the cache length counters[1]; start only picks the
+// decode plan, and no buffer may need to grow.
+int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, int t, int start, bool all_logits,
+                   int *counters = nullptr) {
     const wick_hip_model_config &c = m->c;
     const hipStream_t s = m->stream;
     RC_TRY(ensure_activations(m, t));
     RC_TRY(ensure_logits(m, all_logits ? t : 1));
-    hipError_t e = wick::launch_embed(m->embed, tok_dev, m->x, t, c.hidden, s);
+    hipError_t e = wick::launch_embed(m->embed, tok_dev, m->x, t, c.hidden, s, counters);
     if (e != hipSuccess) return hip_fail(e, "embed kernel launch");
     for (int li = 0; li < c.layers; li++) {
         const wick_hip_model::Layer &L = m->layers[li];
@@ -208,7 +213,7 @@ int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, 
         g.t = t;
         RC_TRY(product(m, wick::kEpiQkv, g, "qkv product launch"));
 
-        RC_TRY(wick::attend_model(kv, li, c.heads, m->q, m->k, m->v, t, start, m->att));
+        RC_TRY(wick::attend_model(kv, li, c.heads, m->q, m->k, m->v, t, start, m->att, counters ? counters + 1 : nullptr));
 
         g = wick::GemvArgs{};
         g.x = m->att;
@@ -262,6 +267,53 @@ int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, 
 int upload_ids(wick_hip_model *m, const uint32_t *ids, int n) {
     HIP_TRY(hipMemcpyAsync(m->ids, ids, (size_t)n * sizeof(uint32_t), hipMemcpyHostToDevice, m->stream));
     HIP_TRY(hipStreamSynchronize(m->stream));
+    return WICK_HIP_OK;
+}
+
+// Shortest run of equal-plan decode steps worth a capture: below it the
+// steps launch directly (capture and instantiation cost about as much as
+// ~20 steps' worth of launch gaps save).
+constexpr int kGraphMinSteps = 24;
+
+// Greedy step i of a decode loop, launched directly: forward of ids[i] at
+// position start + i, argmax into ids[i + 1].
+int decode_step(wick_hip_model *m, wick_hip_kv *kv, int start, int i) {
+    RC_TRY(forward_device(m, kv, m->ids + i, 1, start + i, false));
+    hipError_t e = wick::launch_argmax(m->logits, m->c.vocab, m->ids + i + 1, m->stream);
+    if (e != hipSuccess) return hip_fail(e, "argmax launch");
+    return WICK_HIP_OK;
+}
+
+// Steps i0..i1-1 (one decode plan) from one captured step replayed as a HIP
+// graph: each replay reads its token index and cache length from
+// m->counters, which its argmax advances.  The graph holds no memset node and
+// is destroyed before returning (it bakes in this call's buffers).
+int decode_replayed(wick_hip_model *m, wick_hip_kv *kv, int start, int i0, int i1) {
+    if (!m->counters) HIP_TRY(hipMalloc(&m->counters, 2 * sizeof(int)));
+    hipGraph_t graph = nullptr;
+    HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+    int rc = forward_device(m, kv, m->ids, 1, start + i0, false, m->counters);
+    if (!rc) {
+        hipError_t e = wick::launch_argmax(m->logits, m->c.vocab, m->ids, m->stream, m->counters, m->counters + 1);
+        if (e != hipSuccess) rc = hip_fail(e, "argmax launch");
+    }
+    hipError_t e = hipStreamEndCapture(m->stream, &graph);
+    if (rc) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    e = wick::launch_set_step(m->counters, i0, start + i0 + 1, m->stream);
+    for (int k = i0; k < i1 && e == hipSuccess; k++) e = hipGraphLaunch(exec, m->stream);
+    // the replays must finish before the graph goes
+    const hipError_t es = hipStreamSynchronize(m->stream);
+    (void)hipGraphExecDestroy(exec);
+    if (e != hipSuccess) return hip_fail(e, "decode step replay");
+    if (es != hipSuccess) return hip_fail(es, "hipStreamSynchronize");
     return WICK_HIP_OK;
 }
 
@@ -372,6 +424,7 @@ void wick_hip_model_destroy(wick_hip_model *m) {
     if (m->logits) (void)hipFree(m->logits);
     if (m->ids) (void)hipFree(m->ids);
     if (m->pinned_id) (void)hipHostFree(m->pinned_id);
+    if (m->counters) (void)hipFree(m->counters);
     for (void *p : m->allocs) (void)hipFree(p);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     delete m;
@@ -437,10 +490,21 @@ int wick_hip_model_decode(wick_hip_model *m, wick_hip_kv *kv, uint32_t first, in
     RC_TRY(check_tokens(m, &first, 1));
     RC_TRY(ensure_ids(m, steps + 1));
     RC_TRY(upload_ids(m, &first, 1));
-    for (int i = 0; i < steps; i++) {
-        RC_TRY(forward_device(m, kv, m->ids + i, 1, start + i, false));
-        hipError_t e = wick::launch_argmax(m->logits, m->c.vocab, m->ids + i + 1, m->stream);
-        if (e != hipSuccess) return hip_fail(e, "argmax launch");
+    int i = 0;
+    while (i < steps) {
+        // steps i..j-1 share the decode plan: all but the first run from one
+        // captured step (the first, launched directly, makes any allocation
+        // the step needs)
+        const long long plan = wick::decode_plan_key(kv, m->c.heads, start + i + 1);
+        int j = i + 1;
+        while (j < steps && wick::decode_plan_key(kv, m->c.heads, start + j + 1) == plan) j++;
+        RC_TRY(decode_step(m, kv, start, i));
+        if (j - i > kGraphMinSteps) {
+            RC_TRY(decode_replayed(m, kv, start, i + 1, j));
+        } else {
+            for (int k = i + 1; k < j; k++) RC_TRY(decode_step(m, kv, start, k));
+        }
+        i = j;
     }
     HIP_TRY(hipMemcpyAsync(out, m->ids + 1, (size_t)steps * sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream));
     HIP_TRY(hipStreamSynchronize(m->stream));

@@ -40,9 +40,16 @@ hipError_t launch_gemm(int epi, const GemvArgs &a, hipStream_t s);
 hipError_t launch_rmsnorm(const float *x, const float *g, float eps, float *out, int t, int n, hipStream_t s);
 
 // x[i][:] = embed[tokens[i]][:] for i < t (token ids already validated).
-hipError_t launch_embed(const float *embed, const uint32_t *tokens, float *x, int t, int hidden, hipStream_t s);
+// step: when non-null, the token of row i is tokens[*step + i] (device counter).
+hipError_t launch_embed(const float *embed, const uint32_t *tokens, float *x, int t, int hidden, hipStream_t s,
+                        const int *step = nullptr);
 
 // *out = sampler::argmax(x[0..n)) (first index of the maximum).
-hipError_t launch_argmax(const float *x, int n, uint32_t *out, hipStream_t s);
+// step, len: when non-null, the id goes to out[*step + 1] and both counters
+// advance by one (the graph-replayed decode loop).
+hipError_t launch_argmax(const float *x, int n, uint32_t *out, hipStream_t s, int *step = nullptr, int *len = nullptr);
+// counters[0] = step, counters[1] = len: the state a replayed decode step reads (a kernel,
+// not a host copy, so the values travel with the launch).
+hipError_t launch_set_step(int *counters, int step, int len, hipStream_t s);
 
 }  // namespace wick
