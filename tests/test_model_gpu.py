@@ -70,6 +70,57 @@ def test_tiny_greedy_on_device(name):
     assert ids == exp["greedy"]
 
 
+@pytest.mark.parametrize("case", ["tie", "nan0", "nan_other", "odd_pairs"])
+def test_device_argmax_edge_cases(case):
+    """The device argmax reduces the LM head's per-4-row (value, index) pairs;
+    sampler::argmax (src/sampler.rs:129-137) keeps the first index of the
+    maximum, never picks a NaN, and never leaves index 0 when its logit is NaN.
+    Rows of the LM head are copied or poisoned so the logits hold exact ties
+    and NaNs; prefill's and decode's ids must equal the oracle's argmax of the
+    logits forward() returns for the same tokens."""
+    import dataclasses
+    cfg, w, exp = fixture("llama3-scaled-f32")
+    w = dict(w)
+    prompt = exp["greedy_prompt"]
+    if case == "odd_pairs":  # 90 rows: 23 pairs, the last of 2 rows
+        cfg = dataclasses.replace(cfg, vocab=90)
+        w["embed"] = np.ascontiguousarray(w["embed"][:90])
+        w["lm_head"] = np.ascontiguousarray(w["lm_head"][:90])
+        prompt = [t % 90 for t in prompt]
+    with DeviceModel(cfg, w) as m:
+        logits = m.forward(m.new_cache(64), prompt)[-1]
+    best = int(np.argmax(logits))
+    head = w["lm_head"].copy()
+    if case == "tie":  # the best row copied to a smaller and a larger index
+        lo = 1 if best != 1 else 2
+        head[lo] = head[best]
+        head[(best + 37) % cfg.vocab] = head[best]
+    elif case == "nan0":
+        head[0, 5] = np.nan
+    elif case == "nan_other":
+        head[best, 5] = np.nan
+    elif case == "odd_pairs":  # the maximum in the last, 2-row pair
+        head[89] = head[best] * (1.5 if logits[best] > 0 else 0.5)
+    w["lm_head"] = head
+    with DeviceModel(cfg, w) as m:
+        want = m.forward(m.new_cache(64), prompt)[-1]
+        tok = ol.argmax(want)
+        cache = m.new_cache(64)
+        first = m.prefill(cache, prompt)
+        nxt = m.decode(cache, first, 2)
+        want2 = m.forward(m.new_cache(64), list(prompt) + [first])[-1]
+    assert first == tok
+    assert nxt[0] == ol.argmax(want2)
+    if case == "tie":
+        assert tok == min(lo, best) and want[lo] == want[best]
+    elif case == "nan0":
+        assert np.isnan(want[0]) and tok == 0
+    elif case == "nan_other":
+        assert np.isnan(want[best]) and (tok != best) == (best != 0)
+    elif case == "odd_pairs":
+        assert tok == 89
+
+
 def oracle_greedy(cfg, w, prompt, n_gen, capacity):
     om = ol.OracleModel(cfg, w)
     st = om.new_state(capacity)

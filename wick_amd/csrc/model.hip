@@ -34,6 +34,15 @@ __device__ __forceinline__ float dot4(const f4 w, const f4 x, float acc) {
     return fmaf(w.w, x.w, acc);
 }
 
+// Keeps (v, i) when v is larger, or equal at a smaller index: the first index
+// of the maximum over the non-NaN values (NaN never compares greater).
+__device__ __forceinline__ void arg_better(float v, int i, float &bv, int &bi) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
 }  // namespace
 
 // One wave per R output rows (rows R*wave .. R*wave+R-1), NT tokens per wave
@@ -142,7 +151,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
             const int row = row0 + r;
             if (row >= a.rows) break;
             const float d = acc[r][tk];
-            if (EPI == kEpiStore) {
+            if (EPI == kEpiStore || EPI == kEpiArgmax) {
                 a.out0[tok * a.ld0 + row] = d;
             } else if (EPI == kEpiResid) {
                 a.out0[tok * a.ld0 + row] = resid + d;
@@ -156,6 +165,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
             } else {  // silu_mul: g / (1 + exp(-g)) * u
                 a.out0[tok * a.ld0 + row] = d / (1.0f + expf(-d)) * acc2[tk];
             }
+        }
+    }
+    if constexpr (EPI == kEpiArgmax) {
+        // the wave's rows in increasing order; argmax_kernel reduces the pairs
+        static_assert(NT == 1 && R == kArgmaxRows, "one token, one pair per kArgmaxRows rows");
+        if (lane == 0) {
+            float bv = -INFINITY;
+            int bi = 0x7fffffff;
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (row0 + r < a.rows) arg_better(acc[r][0], row0 + r, bv, bi);
+            reinterpret_cast<float2 *>(a.out1)[row0 / R] = make_float2(bv, __int_as_float(bi));
         }
     }
 }
@@ -291,45 +312,65 @@ __global__ __launch_bounds__(256) void embed_kernel(const float *__restrict__ em
 // { best = i }.  That is the first index of the maximum over the non-NaN
 // values (NaN never compares greater), except that a NaN at index 0 is never
 // replaced.  One workgroup; each thread issues 8 float4 loads per pass before
-// comparing, so a 49152-entry vocabulary is one memory round trip.  Ties
-// resolve to the smaller index.
-__device__ __forceinline__ void arg_better(float v, int i, float &bv, int &bi) {
-    if (v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
-    }
-}
+// comparing.  Ties resolve to the smaller index.  With parts (the LM head's
+// kEpiArgmax pairs, one per kArgmaxRows rows) the workgroup reduces those
+// instead: a quarter of the values, each 2 floats, and every pair's index the
+// smallest among its rows' maxima, so the result is the same.
 
 // step, len (graph-replayed decode loop): the id goes to out[*step + 1], then
 // *step and *len advance to the next forward's token and cache length.
 __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ x, int n, uint32_t *__restrict__ out,
-                                                      int *__restrict__ step, int *__restrict__ len) {
+                                                      int *__restrict__ step, int *__restrict__ len,
+                                                      const float *__restrict__ parts) {
     constexpr int U = 8;
     __shared__ float sv[16];
     __shared__ int si[16];
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    const int n4 = n >> 2;
-    const f4 *x4 = reinterpret_cast<const f4 *>(x);
-    for (int base = threadIdx.x; base < n4; base += U * 1024) {
-        f4 v[U];
+    if (parts) {
+        // two pairs per float4
+        const int np = argmax_parts(n), np2 = np >> 1;
+        const f4 *p4 = reinterpret_cast<const f4 *>(parts);
+        for (int base = threadIdx.x; base < np2; base += U * 1024) {
+            f4 v[U];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int c = base + 1024 * u;
-            v[u] = c < n4 ? x4[c] : f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-        }
+            for (int u = 0; u < U; u++) {
+                const int c = base + 1024 * u;
+                if (c < np2) v[u] = p4[c];
+            }
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int c = base + 1024 * u;
-            if (c < n4) {
-                arg_better(v[u].x, 4 * c, bv, bi);
-                arg_better(v[u].y, 4 * c + 1, bv, bi);
-                arg_better(v[u].z, 4 * c + 2, bv, bi);
-                arg_better(v[u].w, 4 * c + 3, bv, bi);
+            for (int u = 0; u < U; u++) {
+                const int c = base + 1024 * u;
+                if (c < np2) {
+                    arg_better(v[u].x, __float_as_int(v[u].y), bv, bi);
+                    arg_better(v[u].z, __float_as_int(v[u].w), bv, bi);
+                }
             }
         }
+        if ((np & 1) && threadIdx.x == 0) arg_better(parts[2 * np - 2], __float_as_int(parts[2 * np - 1]), bv, bi);
+    } else {
+        const int n4 = n >> 2;
+        const f4 *x4 = reinterpret_cast<const f4 *>(x);
+        for (int base = threadIdx.x; base < n4; base += U * 1024) {
+            f4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int c = base + 1024 * u;
+                v[u] = c < n4 ? x4[c] : f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int c = base + 1024 * u;
+                if (c < n4) {
+                    arg_better(v[u].x, 4 * c, bv, bi);
+                    arg_better(v[u].y, 4 * c + 1, bv, bi);
+                    arg_better(v[u].z, 4 * c + 2, bv, bi);
+                    arg_better(v[u].w, 4 * c + 3, bv, bi);
+                }
+            }
+        }
+        for (int i = 4 * n4 + threadIdx.x; i < n; i += 1024) arg_better(x[i], i, bv, bi);
     }
-    for (int i = 4 * n4 + threadIdx.x; i < n; i += 1024) arg_better(x[i], i, bv, bi);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
         const float ov = __shfl_xor(bv, off, 64);
@@ -377,9 +418,14 @@ hipError_t gemv_launch(const GemvArgs &a, hipStream_t s) {
 // flight per wave.  Several tokens: 4 per wave, 4 float4s per lane per pass.
 template <int EPI>
 hipError_t gemv_epi(const GemvArgs &a, hipStream_t s) {
-    if (a.t > 1) return gemv_launch<4, 1, 4, EPI>(a, s);
-    if constexpr (EPI == kEpiStore) return gemv_launch<1, 4, 4, EPI>(a, s);
-    return gemv_launch<1, 1, 8, EPI>(a, s);
+    if constexpr (EPI == kEpiArgmax) {
+        if (a.t != 1 || !a.out1) return hipErrorInvalidValue;
+        return gemv_launch<1, kArgmaxRows, 4, EPI>(a, s);
+    } else {
+        if (a.t > 1) return gemv_launch<4, 1, 4, EPI>(a, s);
+        if constexpr (EPI == kEpiStore) return gemv_launch<1, 4, 4, EPI>(a, s);
+        return gemv_launch<1, 1, 8, EPI>(a, s);
+    }
 }
 
 }  // namespace
@@ -391,6 +437,7 @@ hipError_t launch_gemv(int epi, const GemvArgs &a, hipStream_t s) {
     case kEpiResid: return gemv_epi<kEpiResid>(a, s);
     case kEpiQkv: return gemv_epi<kEpiQkv>(a, s);
     case kEpiSwiglu: return gemv_epi<kEpiSwiglu>(a, s);
+    case kEpiArgmax: return gemv_epi<kEpiArgmax>(a, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -433,8 +480,8 @@ hipError_t launch_set_step(int *counters, int step, int len, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float *x, int n, uint32_t *out, hipStream_t s, int *step, int *len) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, x, n, out, step, len);
+hipError_t launch_argmax(const float *x, int n, uint32_t *out, hipStream_t s, int *step, int *len, const float *parts) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, x, n, out, step, len, parts);
     return hipGetLastError();
 }
 

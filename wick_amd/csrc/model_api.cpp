@@ -72,6 +72,7 @@ struct wick_hip_model {
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *h = nullptr;
     int cap_logits = 0;  // rows of logits
     float *logits = nullptr;
+    float *argparts = nullptr;  // the LM head's argmax pairs for the last token (argmax_parts(vocab) of them)
     int cap_ids = 0;
     uint32_t *ids = nullptr;  // token ids on the device (prompt, or the greedy chain)
     uint32_t *pinned_id = nullptr;  // page-locked slot the generate loop reads ids through
@@ -121,6 +122,8 @@ int ensure_activations(wick_hip_model *m, int t) {
 }
 
 int ensure_logits(wick_hip_model *m, int rows) {
+    if (!m->argparts)
+        HIP_TRY(hipMalloc(&m->argparts, (size_t)2 * wick::argmax_parts(m->c.vocab) * sizeof(float)));
     if (rows <= m->cap_logits) return WICK_HIP_OK;
     HIP_TRY(hipStreamSynchronize(m->stream));
     if (m->logits) (void)hipFree(m->logits);
@@ -258,7 +261,12 @@ int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, 
     g.rows = c.vocab;
     g.cols = c.hidden;
     g.t = all_logits ? t : 1;
-    RC_TRY(product(m, wick::kEpiStore, g, "lm head product launch"));
+    if (all_logits) {
+        RC_TRY(product(m, wick::kEpiStore, g, "lm head product launch"));
+    } else {
+        g.out1 = m->argparts;  // the first greedy step rides along with the product
+        RC_TRY(product(m, wick::kEpiArgmax, g, "lm head product launch"));
+    }
     return WICK_HIP_OK;
 }
 
@@ -279,7 +287,7 @@ constexpr int kGraphMinSteps = 24;
 // position start + i, argmax into ids[i + 1].
 int decode_step(wick_hip_model *m, wick_hip_kv *kv, int start, int i) {
     RC_TRY(forward_device(m, kv, m->ids + i, 1, start + i, false));
-    hipError_t e = wick::launch_argmax(m->logits, m->c.vocab, m->ids + i + 1, m->stream);
+    hipError_t e = wick::launch_argmax(m->logits, m->c.vocab, m->ids + i + 1, m->stream, nullptr, nullptr, m->argparts);
     if (e != hipSuccess) return hip_fail(e, "argmax launch");
     return WICK_HIP_OK;
 }
@@ -294,7 +302,8 @@ int decode_replayed(wick_hip_model *m, wick_hip_kv *kv, int start, int i0, int i
     HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
     int rc = forward_device(m, kv, m->ids, 1, start + i0, false, m->counters);
     if (!rc) {
-        hipError_t e = wick::launch_argmax(m->logits, m->c.vocab, m->ids, m->stream, m->counters, m->counters + 1);
+        hipError_t e =
+            wick::launch_argmax(m->logits, m->c.vocab, m->ids, m->stream, m->counters, m->counters + 1, m->argparts);
         if (e != hipSuccess) rc = hip_fail(e, "argmax launch");
     }
     hipError_t e = hipStreamEndCapture(m->stream, &graph);
@@ -422,6 +431,7 @@ void wick_hip_model_destroy(wick_hip_model *m) {
     if (m->stream) (void)hipStreamSynchronize(m->stream);
     free_activations(m);
     if (m->logits) (void)hipFree(m->logits);
+    if (m->argparts) (void)hipFree(m->argparts);
     if (m->ids) (void)hipFree(m->ids);
     if (m->pinned_id) (void)hipHostFree(m->pinned_id);
     if (m->counters) (void)hipFree(m->counters);
@@ -476,7 +486,7 @@ int wick_hip_model_prefill(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *p
         const int t = std::min(kPrefillChunk, n - off);
         RC_TRY(forward_device(m, kv, m->ids + off, t, start + off, false));
     }
-    hipError_t e = wick::launch_argmax(m->logits, m->c.vocab, m->ids + n, m->stream);
+    hipError_t e = wick::launch_argmax(m->logits, m->c.vocab, m->ids + n, m->stream, nullptr, nullptr, m->argparts);
     if (e != hipSuccess) return hip_fail(e, "argmax launch");
     HIP_TRY(hipMemcpyAsync(next, m->ids + n, sizeof(uint32_t), hipMemcpyDeviceToHost, m->stream));
     HIP_TRY(hipStreamSynchronize(m->stream));

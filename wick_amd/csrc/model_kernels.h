@@ -14,7 +14,13 @@ enum GemvEpilogue {
     kEpiResid = 1,   // out0[tok][row] += dot            (the residual adds of src/model.rs:487, :503)
     kEpiQkv = 2,     // rows split over out0 / out1 / out2 (q, k, v of src/model.rs:452-462)
     kEpiSwiglu = 3,  // out0[tok][row] = silu(dot_w) * dot_w2   (silu_mul, src/kernels.rs:373-378)
+    kEpiArgmax = 4,  // kEpiStore for one token, and the first greedy step: out1 gets one
+                     // (value, index) pair per kArgmaxRows rows, see launch_argmax
 };
+
+// Logit rows per argmax partial (the LM head's rows per wave).
+constexpr int kArgmaxRows = 4;
+__host__ __device__ inline int argmax_parts(int rows) { return (rows + kArgmaxRows - 1) / kArgmaxRows; }
 
 struct GemvArgs {
     const float *x;       // input rows [t][cols]
@@ -47,7 +53,11 @@ hipError_t launch_embed(const float *embed, const uint32_t *tokens, float *x, in
 // *out = sampler::argmax(x[0..n)) (first index of the maximum).
 // step, len: when non-null, the id goes to out[*step + 1] and both counters
 // advance by one (the graph-replayed decode loop).
-hipError_t launch_argmax(const float *x, int n, uint32_t *out, hipStream_t s, int *step = nullptr, int *len = nullptr);
+// parts: when non-null, the argmax_parts(n) pairs the kEpiArgmax product wrote
+// for x (pair p: the best of rows kArgmaxRows*p.., as value and the index's
+// bits), which are reduced instead of the n logits.
+hipError_t launch_argmax(const float *x, int n, uint32_t *out, hipStream_t s, int *step = nullptr, int *len = nullptr,
+                         const float *parts = nullptr);
 // counters[0] = step, counters[1] = len: the state a replayed decode step reads (a kernel,
 // not a host copy, so the values travel with the launch).
 hipError_t launch_set_step(int *counters, int step, int len, hipStream_t s);
