@@ -34,6 +34,31 @@ def test_library_exports_every_symbol():
         assert hasattr(lib, name), name
 
 
+def test_integration_build_rs_lists_every_source():
+    """The build.rs that INTEGRATION.md gives the Rust side compiles exactly the
+    sources wick_amd/build.py builds libwick_hip.so from."""
+    from wick_amd import build
+    with open(os.path.join(ROOT, "INTEGRATION.md")) as f:
+        text = f.read()
+    block = re.search(r"## 1\. `build\.rs`.*?```rust\n(.*?)```", text, re.S)
+    assert block, "INTEGRATION.md has no build.rs block"
+    listed = re.findall(r'"(wick_amd/csrc/[\w.]+)"', block.group(1))
+    assert len(listed) == len(set(listed)), listed
+    assert sorted(listed) == sorted(build.HIP_SOURCES)
+    for src in build.HIP_SOURCES:
+        assert os.path.exists(os.path.join(ROOT, src)), src
+
+
+def test_library_leaves_no_internal_symbol_undefined():
+    """Every wick_hip_* and wick:: symbol the library uses is defined in it: a
+    source missing from the build list shows up here (as it would at link time)."""
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--undefined-only", _native.HIP_LIB], check=True,
+                         stdout=subprocess.PIPE, text=True).stdout
+    missing = [l.split()[-1] for l in out.splitlines() if "wick_hip_" in l or "4wick" in l]
+    assert not missing, missing
+
+
 def test_argument_errors_without_device_work():
     lib = _native.load()
     h = ctypes.c_void_p()

@@ -29,10 +29,22 @@ def _run(cmd):
         raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}")
 
 
+# Every source of libwick_hip.so, relative to the repository root.  A Rust
+# build.rs that compiles the library lists exactly these files.
+HIP_SOURCES = (
+    "wick_amd/csrc/attention.hip",
+    "wick_amd/csrc/prep.hip",
+    "wick_amd/csrc/model.hip",
+    "wick_amd/csrc/sampler.hip",
+    "wick_amd/csrc/api.cpp",
+    "wick_amd/csrc/model_api.cpp",
+    "wick_amd/csrc/sampler_api.cpp",
+)
+
+
 def build_hip():
     out = os.path.join(HERE, "libwick_hip.so")
-    srcs = [os.path.join(CSRC, f) for f in ("attention.hip", "prep.hip", "model.hip", "sampler.hip", "api.cpp", "model_api.cpp",
-                                             "sampler_api.cpp")]
+    srcs = [os.path.join(ROOT, f) for f in HIP_SOURCES]
     _run([HIPCC, *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", out + ".tmp"])
     os.replace(out + ".tmp", out)
     return out

@@ -50,29 +50,56 @@ class Config:
                 "Qwen2ForCausalLM": "qwen2", "qwen2": "qwen2", "Qwen3ForCausalLM": "qwen3", "qwen3": "qwen3"}.get(name)
         if arch is None:
             raise ValueError(f"unsupported architecture {name}")
-        heads = j["num_attention_heads"]
+        def need(k):
+            v = j.get(k)
+            if not isinstance(v, int) or isinstance(v, bool) or v < 0:
+                raise ValueError(f"config.json: missing {k}")
+            return v
+        hidden = need("hidden_size")
+        heads = need("num_attention_heads")
         kv_heads = j.get("num_key_value_heads") or heads
-        hidden = j["hidden_size"]
         head_dim = j.get("head_dim") or hidden // heads
+        act = j.get("hidden_act")
+        if isinstance(act, str) and act != "silu":
+            # src/config.rs:74-78: only SwiGLU (silu) FFNs are implemented
+            raise ValueError(f"unsupported activation {act}")
+        # transformers 5 writes rope_parameters (rope_theta inside); older configs
+        # have top-level rope_theta and rope_scaling.  Only a missing or null
+        # rope_scaling falls back to rope_parameters (src/config.rs:81-89).
         rp = j.get("rope_parameters")
         theta = j.get("rope_theta")
-        if theta is None and rp:
-            theta = rp.get("rope_theta")
-        rs = j.get("rope_scaling") or rp
+        if not isinstance(theta, (int, float)) or isinstance(theta, bool):
+            theta = rp.get("rope_theta") if isinstance(rp, dict) else None
+            if not isinstance(theta, (int, float)) or isinstance(theta, bool):
+                theta = None
+        rs = j.get("rope_scaling")
+        if rs is None:
+            rs = rp
         scaling = None
-        if rs:
-            kind = rs.get("rope_type") or rs.get("type") or "default"
+        if rs is not None:
+            kind = None
+            if isinstance(rs, dict):
+                kind = rs["rope_type"] if "rope_type" in rs else rs.get("type")
+            if not isinstance(kind, str):
+                kind = "default"
             if kind == "llama3":
-                scaling = RopeScaling(float(np.float32(rs["factor"])), float(np.float32(rs["low_freq_factor"])),
-                                      float(np.float32(rs["high_freq_factor"])),
-                                      int(rs["original_max_position_embeddings"]))
+                def f(k):
+                    v = rs.get(k)
+                    if not isinstance(v, (int, float)) or isinstance(v, bool):
+                        raise ValueError(f"rope_scaling: missing {k}")
+                    return v
+                scaling = RopeScaling(float(np.float32(f("factor"))), float(np.float32(f("low_freq_factor"))),
+                                      float(np.float32(f("high_freq_factor"))),
+                                      int(f("original_max_position_embeddings")))
             elif kind != "default":
-                raise ValueError(f"unsupported rope_scaling type {kind}")
+                raise ValueError(f"unsupported rope_scaling type {kind!r}")
         eos = j.get("eos_token_id")
-        cfg = Config(arch=arch, hidden=hidden, intermediate=j["intermediate_size"], layers=j["num_hidden_layers"],
-                     heads=heads, kv_heads=kv_heads, head_dim=head_dim, vocab=j["vocab_size"],
+        eps = j.get("rms_norm_eps")
+        cfg = Config(arch=arch, hidden=hidden, intermediate=need("intermediate_size"), layers=need("num_hidden_layers"),
+                     heads=heads, kv_heads=kv_heads, head_dim=head_dim, vocab=need("vocab_size"),
                      max_position=j.get("max_position_embeddings") or 4096,
-                     rms_eps=float(np.float32(j.get("rms_norm_eps", 1e-6))),
+                     rms_eps=float(np.float32(eps if isinstance(eps, (int, float)) and not isinstance(eps, bool)
+                                              else 1e-6)),
                      rope_theta=float(np.float32(theta if theta is not None else 10000.0)),
                      rope_scaling=scaling, tie_embeddings=bool(j.get("tie_word_embeddings", False)),
                      attn_bias=arch == "qwen2" or bool(j.get("attention_bias", False)), qk_norm=arch == "qwen3",
@@ -157,6 +184,25 @@ def load_safetensors(path):
     return out
 
 
+def load_safetensors_dir(d):
+    """Every tensor of a model directory: model.safetensors, or each shard that
+    model.safetensors.index.json's weight_map names, merged into one dict
+    (SafeTensors::open_dir, src/safetensors.rs:56-75: shards in sorted order,
+    each opened once, a later shard's tensor replacing an earlier one's)."""
+    index = os.path.join(d, "model.safetensors.index.json")
+    if not os.path.exists(index):
+        return load_safetensors(os.path.join(d, "model.safetensors"))
+    with open(index) as f:
+        j = json.load(f)
+    wm = j.get("weight_map") if isinstance(j, dict) else None
+    if not isinstance(wm, dict):
+        raise ValueError(f"{index}: index has no weight_map")
+    out = {}
+    for shard in sorted({v for v in wm.values() if isinstance(v, str)}):
+        out.update(load_safetensors(os.path.join(d, shard)))
+    return out
+
+
 LAYER_TENSORS = ("attn_norm", "wq", "wk", "wv", "wo", "bq", "bk", "bv", "q_norm", "k_norm", "ffn_norm", "w_gate",
                  "w_up", "w_down")
 _HF = {"attn_norm": "input_layernorm.weight", "wq": "self_attn.q_proj.weight", "wk": "self_attn.k_proj.weight",
@@ -168,7 +214,7 @@ _HF = {"attn_norm": "input_layernorm.weight", "wq": "self_attn.q_proj.weight", "
 
 def load_weights(d, cfg):
     """f32 weights in wick's naming (Model::from_tensors, src/model.rs:178-235), with shape checks."""
-    st = load_safetensors(os.path.join(d, "model.safetensors"))
+    st = load_safetensors_dir(d)
     h, q, kv, ff = cfg.hidden, cfg.q_dim, cfg.kv_dim, cfg.intermediate
     shapes = {"attn_norm": (h,), "wq": (q, h), "wk": (kv, h), "wv": (kv, h), "wo": (h, q), "bq": (q,), "bk": (kv,),
               "bv": (kv,), "q_norm": (cfg.head_dim,), "k_norm": (cfg.head_dim,), "ffn_norm": (h,),
