@@ -76,6 +76,22 @@ int wick_hip_kv_append_device(wick_hip_kv *kv, int layer, int start, int t, cons
 int wick_hip_attention_device(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int t, int start,
                               float *att_dev);
 
+/* As wick_hip_attention_device, but it allocates nothing: no hipMalloc, hipFree
+ * or allocating library call on any call, the first included.  No counterpart
+ * in the reference; it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid it).
+ * Single-token decode keeps its split-K partial states in a static 32 MiB
+ * device array (one per GPU, held until the process ends) instead of the
+ * handle's workspace: it needs kv_heads * ceil(group / 16) * 16 * 256 *
+ * (head_dim + 2) floats, at most 8 Mi (e.g. up to 31 kv heads at head_dim 64
+ * with group <= 16, or 15 at head_dim 128); a larger shape returns
+ * WICK_HIP_EINVAL.  Prefill (t > 1) uses no workspace.  Every call on one GPU
+ * shares that array, so calls that overlap on one GPU (other handles or
+ * streams included) race: serialise them.  Asynchronous on the handle's
+ * stream. */
+int wick_hip_attention_device_noalloc(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int t, int start,
+                                      float *att_dev);
+
 /* ---- input preparation on the device: the per-token part of Model::forward
  *      that produces what attention reads (src/model.rs:464-484): bias add,
  *      QK-norm, RoPE of q and k, and the cache append.  The prepared q and the

@@ -69,6 +69,7 @@ def test_argument_errors_without_device_work():
     lib.wick_hip_kv_destroy(None)
     assert lib.wick_hip_kv_set_option(None, 1, 64) == _native.EINVAL
     assert lib.wick_hip_attention(None, 0, 4, None, 1, 0, None) == _native.EINVAL
+    assert lib.wick_hip_attention_device_noalloc(None, 0, 4, None, 1, 0, None) == _native.EINVAL
     assert lib.wick_hip_kv_last_grid(None) == 0
     assert lib.wick_hip_kv_set_rope(None, None) == _native.EINVAL
     assert lib.wick_hip_kv_set_prep(None, 0, 4, None, None, None, None, None, ctypes.c_float(1e-6)) == _native.EINVAL

@@ -33,6 +33,7 @@ SIGNATURES = {
     "wick_hip_last_error": (ctypes.c_char_p, []),
     "wick_hip_kv_append_device": (_I, [_P, _I, _I, _I, _P, _P]),
     "wick_hip_attention_device": (_I, [_P, _I, _I, _P, _I, _I, _P]),
+    "wick_hip_attention_device_noalloc": (_I, [_P, _I, _I, _P, _I, _I, _P]),
     "wick_hip_kv_set_stream": (_I, [_P, _P]),
     "wick_hip_kv_synchronize": (_I, [_P]),
     "wick_hip_kv_set_option": (_I, [_P, _I, _I]),

@@ -57,6 +57,8 @@ struct wick_hip_kv {
     // decode split-K workspace (partial softmax states of the chunks)
     float *part = nullptr;
     int ws_units = 0;
+    // whether the static workspace's address was found on this device
+    hipError_t static_rc = hipErrorNotInitialized;
     // options
     int decode_chunk = 0, pairing = -1, prefill_split = 1, last_grid = 0;
     int decode_blocks_per_cu = 1, prefill_blocks_per_cu = 1, prefill2_blocks_per_cu = 1;
@@ -153,19 +155,30 @@ void plan_chunks(const wick_hip_kv *kv, int units, int len, int *chunk_out, int 
 
 // Split-K schedule of one decode call over len positions: fills the shape
 // fields of *a and kv->last_grid.
+// static_part: the partial states go to the static workspace (no allocation)
+// instead of the handle's own.
 int plan_decode(wick_hip_kv *kv, int layer, int group, int len, const float *q_dev, float *att_dev,
-                wick::DecodeArgs *a) {
+                wick::DecodeArgs *a, float *static_part = nullptr) {
     const int hslices = (group + wick::kTileRows - 1) / wick::kTileRows;
     const int units = kv->kv_heads * hslices;
-    int rc = ensure_workspace(kv, units);
-    if (rc) return rc;
+    if (static_part) {
+        const size_t need = wick::decode_workspace_floats(units, kv->head_dim);
+        if (need > wick::kStaticScratchFloats)
+            return fail(WICK_HIP_EINVAL,
+                        "decode needs %zu floats of workspace for %d kv heads x %d head slices at head_dim %d; the "
+                        "static workspace holds %zu",
+                        need, kv->kv_heads, hslices, kv->head_dim, wick::kStaticScratchFloats);
+    } else {
+        int rc = ensure_workspace(kv, units);
+        if (rc) return rc;
+    }
     int chunk, nchunks;
     plan_chunks(kv, units, len, &chunk, &nchunks);
     a->q = q_dev;
     a->k = kv->k_layer(layer);
     a->v = kv->v_layer(layer);
     a->att = att_dev;
-    a->part = kv->part;
+    a->part = static_part ? static_part : kv->part;
     a->capacity = kv->capacity;
     a->len = len;
     a->kv_heads = kv->kv_heads;
@@ -177,7 +190,8 @@ int plan_decode(wick_hip_kv *kv, int layer, int group, int len, const float *q_d
     return WICK_HIP_OK;
 }
 
-int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int t, int start, float *att_dev) {
+int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int t, int start, float *att_dev,
+                  float *static_part = nullptr) {
     const int D = kv->head_dim;
     if (heads < 1 || heads % kv->kv_heads != 0)
         return fail(WICK_HIP_EINVAL, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv->kv_heads);
@@ -186,7 +200,7 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
 
     if (t == 1) {
         wick::DecodeArgs a{};
-        int rc = plan_decode(kv, layer, group, start + 1, q_dev, att_dev, &a);
+        int rc = plan_decode(kv, layer, group, start + 1, q_dev, att_dev, &a, static_part);
         if (rc) return rc;
         a.scale = scale;
         hipError_t e = wick::launch_decode(D, a, kv->last_grid, kv->stream);
@@ -391,6 +405,8 @@ int wick_hip_kv_create(int layers, int capacity, int kv_heads, int head_dim, wic
             break;
         }
         kv->num_cus = prop.multiProcessorCount;
+        // the no-allocation entry point's workspace on this device (resolved once)
+        kv->static_rc = wick::static_scratch_init(kv->device);
         kv->prep.resize(layers);
         kv->decode_blocks_per_cu = wick::decode_blocks_per_cu(head_dim);
         kv->prefill_blocks_per_cu = wick::prefill_blocks_per_cu(head_dim, 0);
@@ -519,6 +535,19 @@ int wick_hip_attention_device(wick_hip_kv *kv, int layer, int heads, const float
     if (!q_dev || !att_dev) return fail(WICK_HIP_EINVAL, "null q or att");
     if ((rc = check_aligned(q_dev, "q_dev")) || (rc = check_aligned(att_dev, "att_dev"))) return rc;
     return run_attention(kv, layer, heads, q_dev, t, start, att_dev);
+}
+
+int wick_hip_attention_device_noalloc(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int t, int start,
+                                      float *att_dev) {
+    int rc = check_kv(kv, layer);
+    if (rc) return rc;
+    if ((rc = check_span(kv, start, t))) return rc;
+    if (!q_dev || !att_dev) return fail(WICK_HIP_EINVAL, "null q or att");
+    if ((rc = check_aligned(q_dev, "q_dev")) || (rc = check_aligned(att_dev, "att_dev"))) return rc;
+    if (kv->static_rc != hipSuccess) return hip_fail(kv->static_rc, "hipGetSymbolAddress(static decode workspace)");
+    float *part = wick::static_scratch(kv->device);
+    if (!part) return fail(WICK_HIP_EHIP, "no static decode workspace on device %d", kv->device);
+    return run_attention(kv, layer, heads, q_dev, t, start, att_dev, part);
 }
 
 int wick_hip_attention(wick_hip_kv *kv, int layer, int heads, const float *q, int t, int start, float *att) {

@@ -34,6 +34,8 @@
 
 #include <math.h>
 
+#include <mutex>
+
 namespace wick {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -1123,6 +1125,43 @@ __global__ __launch_bounds__(256) void append_kernel(const AppendArgs a) {
         *reinterpret_cast<f4 *>(a.k + dst) = *reinterpret_cast<const f4 *>(a.ksrc + src);
         *reinterpret_cast<f4 *>(a.v + dst) = *reinterpret_cast<const f4 *>(a.vsrc + src);
     }
+}
+
+// ------------------------------------------------------------------ static decode workspace
+//
+// The split-K partial states of wick_hip_attention_device_noalloc live in this
+// file-scope array instead of a hipMalloc'd buffer, so that entry point never
+// allocates.  Every GPU the library runs on holds its own copy until the
+// process ends; all calls on one GPU share it, so such calls must not overlap.
+// Host code never uses the array's name as an address: kernels receive the
+// per-device address hipGetSymbolAddress returns (static_scratch_init).
+static __device__ __align__(256) float scratch[kStaticScratchFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_rc[kMaxDevices];
+bool g_scratch_done[kMaxDevices];
+}  // namespace
+
+hipError_t static_scratch_init(int device) {
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_done[device]) {
+        // the caller has made `device` current
+        void *p = nullptr;
+        g_scratch_rc[device] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_ptr[device] = g_scratch_rc[device] == hipSuccess ? static_cast<float *>(p) : nullptr;
+        g_scratch_done[device] = true;
+    }
+    return g_scratch_rc[device];
+}
+
+float *static_scratch(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return g_scratch_done[device] ? g_scratch_ptr[device] : nullptr;
 }
 
 // ------------------------------------------------------------------ launchers

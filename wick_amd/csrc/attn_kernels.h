@@ -71,6 +71,15 @@ struct PrepArgs {
 // Floats of decode workspace needed for `units` (kv head, head slice) pairs.
 size_t decode_workspace_floats(int units, int head_dim);
 
+// The static decode workspace of wick_hip_attention_device_noalloc: a
+// file-scope __device__ array of this many floats (32 MiB) on every device.
+constexpr size_t kStaticScratchFloats = size_t(8) << 20;
+// Resolve the array's address on `device`, which must be current; once per
+// device (later calls return the first result).
+hipError_t static_scratch_init(int device);
+// The address static_scratch_init found on `device`, or null.
+float *static_scratch(int device);
+
 // Decode workgroups one CU holds at once (from the kernel's register and LDS use).
 int decode_blocks_per_cu(int head_dim);
 // The same for the split prefill kernel.

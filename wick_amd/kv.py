@@ -121,6 +121,12 @@ class DeviceKvCache:
         _native.check(self._lib.wick_hip_attention_device(self.handle, layer, heads, ctypes.c_void_p(q_ptr), t, start,
                                                           ctypes.c_void_p(att_ptr)))
 
+    def attention_device_noalloc(self, layer, heads, q_ptr, t, start, att_ptr):
+        """attention_device through the entry point that allocates nothing (its
+        decode workspace is a static per-GPU array shared by every such call)."""
+        _native.check(self._lib.wick_hip_attention_device_noalloc(self.handle, layer, heads, ctypes.c_void_p(q_ptr), t,
+                                                                  start, ctypes.c_void_p(att_ptr)))
+
     def set_stream(self, stream_ptr):
         _native.check(self._lib.wick_hip_kv_set_stream(self.handle, ctypes.c_void_p(stream_ptr)))
 
