@@ -97,6 +97,84 @@ def time_launches(torch, fn, launches_per_step, steps, warmup):
     return ms / steps, ms / (steps * launches_per_step)
 
 
+def time_graph(torch, stream, fn, launches_per_step, steps, warmup):
+    """fn (launches_per_step launches on `stream`) captured once as a HIP graph and
+    replayed: returns (ms per step, ms per launch), HIP events on `stream`."""
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    torch.cuda.synchronize()
+    out = time_launches(torch, g.replay, launches_per_step, steps, warmup)
+    del g
+    return out
+
+
+def measure_ceiling(torch, stream, dev, nbytes, layers, steps, warmup):
+    """Practical ceilings of one decode layer's launch on this box, timed like the
+    decode itself (one launch per layer over its own buffer, graph-replayed):
+    the read-only probe over `layers` distinct buffers of nbytes (the layer's K+V
+    bytes) at several grids and both access patterns, and the launch-to-launch
+    floor of an empty kernel on the decode's and the merge's grids."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "wick_amd", "libwick_probe.so"))
+    lib.wick_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                    ctypes.c_void_p]
+    lib.wick_probe_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
+    s = stream.cuda_stream
+    bufs = [torch.ones(nbytes // 4, device=dev) for _ in range(layers)]
+    sink = torch.ones(4096, device=dev)
+    reads = []
+    for strided in (0, 1):
+        for grid in (256, 512, 1024, 2048):
+            def step(grid=grid, strided=strided):
+                for b in bufs:
+                    rc = lib.wick_probe_read(b.data_ptr(), nbytes, grid, strided, sink.data_ptr(), s)
+                    if rc:
+                        raise RuntimeError(f"wick_probe_read: HIP error {rc}")
+            _, ms = time_graph(torch, stream, step, layers, steps, warmup)
+            reads.append({"pattern": "strided" if strided else "slice per workgroup", "workgroups": grid,
+                          "us_per_launch": round(ms * 1e3, 3), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+    floors = {}
+    for grid in (512, 56):
+        def empty(grid=grid):
+            for _ in range(layers):
+                lib.wick_probe_empty(grid, s)
+        _, ms = time_graph(torch, stream, empty, layers, steps, warmup)
+        floors[str(grid)] = round(ms * 1e3, 3)
+    del bufs
+    best = max(reads, key=lambda r: r["GBps"])
+    return {"read_ceiling_GBps": best["GBps"], "read_ceiling_us": best["us_per_launch"], "best": best,
+            "reads": reads, "empty_kernel_us": floors,
+            "method": f"read-only probe (libwick_probe.so) over {layers} distinct buffers of {nbytes} B (the layer's "
+                      f"K+V bytes), one launch per buffer, replayed from a HIP graph, HIP events on the launch "
+                      f"stream; empty kernel launch to launch on 512 and 56 workgroups the same way"}
+
+
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "pmc_traffic_decode64_qwen25_32k.json")
+TRAFFIC_SOURCE = "wick_amd/csrc/attention.hip"
+
+
+def source_sha16(rel):
+    import hashlib
+    with open(os.path.join(ROOT, rel), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def traffic_record():
+    """(HBM bytes per decode call from the committed --pmc summary, where they come
+    from); bytes are None when the summary was measured on another kernel source."""
+    if not os.path.exists(TRAFFIC_JSON):
+        return None, None
+    with open(TRAFFIC_JSON) as f:
+        j = json.load(f)
+    src = {"file": os.path.relpath(TRAFFIC_JSON, ROOT), "measured_on_source": j.get("kernel_source"),
+           "measured_on_sha16": j.get("kernel_source_sha16"), "measured_at_commit": j.get("commit"),
+           "current_sha16": source_sha16(TRAFFIC_SOURCE)}
+    src["matches_current_source"] = src["measured_on_sha16"] == src["current_sha16"]
+    return (j.get("traffic_bytes_per_launch") if src["matches_current_source"] else None), src
+
+
 COPY_MIB = 256
 
 
@@ -342,6 +420,7 @@ def main():
                          "and a 256 MiB device copy that calibrates the byte counters; 'prefill' = 3 launches of "
                          "configs[2] at T=2048")
     ap.add_argument("--decode-chunk", type=int, default=0)
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the read-ceiling / launch-floor probe")
     ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -389,8 +468,9 @@ def main():
     ms_step, ms_launch = ms_step_eager, ms_launch_eager
     if not args.eager:
         # One step (24 launches) captured as a HIP graph and replayed: the way a
-        # GPU-resident decode loop issues its per-token work.  The decode kernel
-        # resets its own merge counters, so replays need no memset nodes.
+        # GPU-resident decode loop issues its per-token work.  A decode call
+        # rewrites every partial state its merge reads and issues no memset or
+        # allocation after its first call, so the graph replays as captured.
         graph = torch.cuda.CUDAGraph()
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=stream):
@@ -427,11 +507,13 @@ def main():
                         "served_from": "HBM" if L == c["L"] else "Infinity Cache (24-layer set < 256 MB)"})
     # HBM bytes per launch measured by the committed rocprofv3 --pmc runs on this
     # same workload (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size).
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "pmc_traffic_decode64_qwen25_32k.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("traffic_bytes_per_launch")
+    # They hold for the kernel source they were measured on: the summary records
+    # that file's hash, and a different source here reports no traffic.
+    traffic, traffic_source = traffic_record()
+    ceiling = None
+    if not args.no_ceiling:
+        ceiling = measure_ceiling(torch, stream, dev, 2 * c["L"] * c["kv_heads"] * c["d"] * 4, c["layers"],
+                                  args.steps, args.warmup)
     bytes_layer = decode_bytes(c["L"], c["heads"], c["kv_heads"], c["d"])
     bytes_step = bytes_layer * c["layers"]
     value = bytes_step / (ms_step * 1e-3) / 1e9
@@ -457,9 +539,14 @@ def main():
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "kernel": "wick::decode_kernel<64, false, false, 4> + wick::decode_merge_kernel<64> (one call)", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "bytes_per_launch": bytes_layer, "us_per_launch": round(ms_launch * 1e3, 3)},
+                     "traffic": traffic, "traffic_source": traffic_source, "bytes_per_launch": bytes_layer,
+                     "us_per_launch": round(ms_launch * 1e3, 3)},
         "decode_lengths": lengths,
     }
+    if ceiling:
+        out["roofline"]["ceiling_GBps"] = ceiling["read_ceiling_GBps"]
+        out["roofline"]["frac_of_ceiling"] = round(achieved / ceiling["read_ceiling_GBps"], 4)
+        out["roofline"]["ceiling"] = ceiling
 
     # ---------------- prefill (configs[2] at T = 512 and 2048; configs[3] chunked)
     if not args.no_prefill:

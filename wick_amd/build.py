@@ -65,9 +65,19 @@ def build_host():
     return out
 
 
+def build_probe():
+    """Measurement kernels for bench.py (read ceiling, launch floor); not part of
+    the attention path."""
+    out = os.path.join(HERE, "libwick_probe.so")
+    _run([HIPCC, *HIP_FLAGS, "-shared", os.path.join(CSRC, "roofline_probe.hip"), "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build_all():
     build_hip()
     build_host()
+    build_probe()
 
 
 if __name__ == "__main__":
