@@ -277,6 +277,18 @@ __device__ __forceinline__ void load_q(const float *qrow, const float *fallback,
     for (int j = 0; j < Shape<D>::KJ; j++) q[j] = *reinterpret_cast<const f4 *>(row + 16 * j + 4 * g) * keep;
 }
 
+// load_q without the padding mask: returns the factor (1 or 0) the caller
+// folds into its own scaling of q, so nothing waits for the loads here.
+template <int D>
+__device__ __forceinline__ float load_q_raw(const float *qrow, const float *fallback, bool valid, int lane,
+                                            f4 (&q)[Shape<D>::KJ]) {
+    const int g = lane >> 4;
+    const float *row = valid ? qrow : fallback;
+#pragma unroll
+    for (int j = 0; j < Shape<D>::KJ; j++) q[j] = *reinterpret_cast<const f4 *>(row + 16 * j + 4 * g);
+    return valid ? 1.f : 0.f;
+}
+
 template <int D>
 __device__ __forceinline__ void init_state(WaveState<D> &st) {
     st.m = -INFINITY;
@@ -396,10 +408,10 @@ __device__ __forceinline__ f4 bload4(__amdgpu_buffer_rsrc_t r, unsigned voff, un
 // A group of TG 16-key tiles for the lean kernels, in the lane layout of
 // load_tiles: lane (i = col, g) holds K[p0 + i][16j + 4g .. +3] and
 // V[p0 + 4g + m][4i + 64 seg .. +3] (head_dim 64 and 128).
-template <int D>
+template <int D, int TG = Shape<D>::TG>
 struct LeanGroup {
-    f4 k[Shape<D>::TG][Shape<D>::KJ];
-    f4 v[Shape<D>::TG][4][Shape<D>::NSEG];
+    f4 k[TG][Shape<D>::KJ];
+    f4 v[TG][4][Shape<D>::NSEG];
 };
 
 // Buffer loads of the group starting at key p0 of the resource's kv head.
@@ -431,17 +443,28 @@ __device__ __forceinline__ void lean_load(__amdgpu_buffer_rsrc_t rk, __amdgpu_bu
 // clamped to kend - 1 when `clamp` (the last group of a range).  Streaming
 // from HBM these run faster than buffer loads (config 2 decode split kernel:
 // 8.5 against 9.2 us).
-template <int D>
-__device__ __forceinline__ void lean_load_global(const float *__restrict__ Kh, const float *__restrict__ Vh, int p0,
-                                                 int kend, bool clamp, int lane, LeanGroup<D> &t) {
+template <int D, int TG = Shape<D>::TG>
+__device__ __forceinline__ void lean_load_global_k(const float *__restrict__ Kh, int p0, int kend, bool clamp,
+                                                   int lane, LeanGroup<D, TG> &t) {
     using S = Shape<D>;
     const int col = lane & 15, g = lane >> 4;
     const int last = clamp ? kend - 1 : 0x7fffffff;
 #pragma unroll
-    for (int u = 0; u < S::TG; u++) {
+    for (int u = 0; u < TG; u++) {
         const float *kr = Kh + (size_t)min(p0 + 16 * u + col, last) * D + 4 * g;
 #pragma unroll
         for (int j = 0; j < S::KJ; j++) t.k[u][j] = *reinterpret_cast<const f4 *>(kr + 16 * j);
+    }
+}
+
+template <int D, int TG = Shape<D>::TG>
+__device__ __forceinline__ void lean_load_global_v(const float *__restrict__ Vh, int p0, int kend, bool clamp,
+                                                   int lane, LeanGroup<D, TG> &t) {
+    using S = Shape<D>;
+    const int col = lane & 15, g = lane >> 4;
+    const int last = clamp ? kend - 1 : 0x7fffffff;
+#pragma unroll
+    for (int u = 0; u < TG; u++) {
 #pragma unroll
         for (int mm = 0; mm < 4; mm++) {
             const float *vr = Vh + (size_t)min(p0 + 16 * u + 4 * g + mm, last) * D + 4 * col;
@@ -449,6 +472,13 @@ __device__ __forceinline__ void lean_load_global(const float *__restrict__ Kh, c
             for (int seg = 0; seg < S::NSEG; seg++) t.v[u][mm][seg] = *reinterpret_cast<const f4 *>(vr + 64 * seg);
         }
     }
+}
+
+template <int D, int TG = Shape<D>::TG>
+__device__ __forceinline__ void lean_load_global(const float *__restrict__ Kh, const float *__restrict__ Vh, int p0,
+                                                 int kend, bool clamp, int lane, LeanGroup<D, TG> &t) {
+    lean_load_global_k<D, TG>(Kh, p0, kend, clamp, lane, t);
+    lean_load_global_v<D, TG>(Vh, p0, kend, clamp, lane, t);
 }
 
 template <int D>
@@ -469,11 +499,10 @@ __device__ __forceinline__ void lean_lane_offsets(int lane, unsigned &vk, unsign
 // T=512 18.5 -> 18.1 us).  Otherwise m is the running max (decode, where the
 // extra test costs more than it saves).  When `masked`, keys at or past this
 // lane's klimit get -inf.
-template <int D, bool LAZY>
-__device__ __forceinline__ void lean_step(const LeanGroup<D> &t, const f4 (&q)[Shape<D>::KJ], int p0, bool masked,
+template <int D, bool LAZY, int TG = Shape<D>::TG>
+__device__ __forceinline__ void lean_step(const LeanGroup<D, TG> &t, const f4 (&q)[Shape<D>::KJ], int p0, bool masked,
                                           int klimit, int g, float &m, float &l, f4 (&o)[Shape<D>::DB]) {
     using S = Shape<D>;
-    constexpr int TG = S::TG;
     float sc[TG][4];
     // Prefill (LAZY): the wave's MFMA bursts run at raised issue priority, so
     // that another wave's softmax fills the gaps rather than competing with
@@ -579,7 +608,9 @@ struct DecodeSpace {
 // NW: waves per workgroup -- 4 for the split schedule; 8 (head_dim <= 64) for
 // a single chunk per unit, so that short contexts give each wave at most one
 // or two tile groups instead of two to four.
-template <int D, bool PREP, bool PP = (D < 128), int NW = 4>
+// TG: 16-key tiles per softmax group of the lean core (head_dim 64 and 128);
+// one tile per group halves the products a wave runs after its last load.
+template <int D, bool PREP, bool PP = (D < 128), int NW = 4, int TG = Shape<D>::TG>
 __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
     using S = Shape<D>;
     __shared__ float sm_m[NW][16], sm_l[NW][16];
@@ -600,6 +631,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
 
     const int col = lane & 15, g = lane >> 4;
     f4 q[S::KJ];
+    float qkeep;  // 0 for the padding columns past the unit's ncols heads
     if constexpr (PREP) {
         // Rows: the unit's ncols q heads (to LDS), then -- in the workgroups
         // of the last chunk, the only ones that read position len-1 -- the new
@@ -624,47 +656,69 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
                               nullptr, nullptr, lane & 15, lane & 48);
         }
         __syncthreads();
-        load_q<D>(sq[col], sq[0], col < ncols, lane, q);
+        qkeep = load_q_raw<D>(sq[col], sq[0], col < ncols, lane, q);
     } else {
-        load_q<D>(a.q + (size_t)(head0 + col) * D, a.q + (size_t)head0 * D, col < ncols, lane, q);
+        qkeep = load_q_raw<D>(a.q + (size_t)(head0 + col) * D, a.q + (size_t)head0 * D, col < ncols, lane, q);
     }
 
     WaveState<D> st;
     if constexpr (D >= 64) {
         // Lean core: q in log2 units, tiles through global loads (keys past
-        // kend clamped and masked in the chunk's last group).
+        // kend clamped and masked in the chunk's last group).  The wave's
+        // first group of tiles is requested before q is scaled, so the stream
+        // of K/V loads does not wait for q's round trip (config 2 split
+        // kernel: the first K loads otherwise went out only after q arrived).
+        const auto scale_q = [&] {
+            const float f = qkeep * (a.scale * kLog2e);
 #pragma unroll
-        for (int j = 0; j < S::KJ; j++) q[j] *= a.scale * kLog2e;
+            for (int j = 0; j < S::KJ; j++) q[j] *= f;
+        };
         st.m = -INFINITY;
         st.l = 0.f;
 #pragma unroll
         for (int db = 0; db < S::DB; db++) st.o[db] = f4{0.f, 0.f, 0.f, 0.f};
-        constexpr int GK = 16 * S::TG;                 // keys per group
+        constexpr int GK = 16 * TG;                 // keys per group
         const int wbeg = __builtin_amdgcn_readfirstlane(kbeg + GK * w), step = NW * GK;
         if constexpr (PP) {
             // the next group's loads go out before this group's products
-            LeanGroup<D> ta, tb;
+            LeanGroup<D, TG> ta, tb;
             int p0 = wbeg;
-            if (p0 < kend) lean_load_global<D>(Kh, Vh, p0, kend, p0 + GK > kend, lane, ta);
+            if (p0 < kend) lean_load_global<D, TG>(Kh, Vh, p0, kend, p0 + GK > kend, lane, ta);
+            __builtin_amdgcn_sched_barrier(0);
+            scale_q();
             while (p0 < kend) {
                 const int p1 = p0 + step;
-                if (p1 < kend) lean_load_global<D>(Kh, Vh, p1, kend, p1 + GK > kend, lane, tb);
-                lean_step<D, false>(ta, q, p0, p0 + GK > kend, kend, g, st.m, st.l, st.o);
+                if (p1 < kend) lean_load_global<D, TG>(Kh, Vh, p1, kend, p1 + GK > kend, lane, tb);
+                lean_step<D, false, TG>(ta, q, p0, p0 + GK > kend, kend, g, st.m, st.l, st.o);
                 if (p1 >= kend) break;
                 const int p2 = p1 + step;
-                if (p2 < kend) lean_load_global<D>(Kh, Vh, p2, kend, p2 + GK > kend, lane, ta);
-                lean_step<D, false>(tb, q, p1, p1 + GK > kend, kend, g, st.m, st.l, st.o);
+                if (p2 < kend) lean_load_global<D, TG>(Kh, Vh, p2, kend, p2 + GK > kend, lane, ta);
+                lean_step<D, false, TG>(tb, q, p1, p1 + GK > kend, kend, g, st.m, st.l, st.o);
                 p0 = p2;
             }
         } else {
-            for (int p0 = wbeg; p0 < kend; p0 += step) {
-                LeanGroup<D> t;
+            int p0 = wbeg;
+            if (p0 < kend) {
+                LeanGroup<D, TG> t;
                 const bool tail = p0 + GK > kend;
-                lean_load_global<D>(Kh, Vh, p0, kend, tail, lane, t);
-                lean_step<D, false>(t, q, p0, tail, kend, g, st.m, st.l, st.o);
+                lean_load_global_k<D, TG>(Kh, p0, kend, tail, lane, t);
+                // keeps the K loads ahead of the wait for q
+                __builtin_amdgcn_sched_barrier(0);
+                scale_q();
+                lean_load_global_v<D, TG>(Vh, p0, kend, tail, lane, t);
+                lean_step<D, false, TG>(t, q, p0, tail, kend, g, st.m, st.l, st.o);
+                p0 += step;
+            }
+            for (; p0 < kend; p0 += step) {
+                LeanGroup<D, TG> t;
+                const bool tail = p0 + GK > kend;
+                lean_load_global<D, TG>(Kh, Vh, p0, kend, tail, lane, t);
+                lean_step<D, false, TG>(t, q, p0, tail, kend, g, st.m, st.l, st.o);
             }
         }
     } else {
+#pragma unroll
+        for (int j = 0; j < S::KJ; j++) q[j] *= qkeep;
         init_state<D>(st);
         attend_range<D, PP>(Kh, Vh, kbeg, kend, w * S::TG, NW * S::TG, len, a.scale, q, lane, st);
         st.m *= kLog2e;  // the merges take maxima in log2 units
@@ -766,14 +820,24 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
     const int grp = tid / DW, dd = tid % DW;
     const int n = a.nchunks;
 
+    // Every child slot ch < kDecodeMaxChunks lies inside the workspace, so the
+    // loads are unconditional (no exec-mask branch per load delays their
+    // issue) and the children past nchunks -- stale or never written -- are
+    // replaced by a select afterwards.
     float vo[NB], vm[NB], vl[NB];
 #pragma unroll
     for (int u = 0; u < NB; u++) {
         const int ch = grp + u * G;
-        const bool live = ch < n;
-        vo[u] = live ? o[(size_t)ch * D + dd] : 0.f;
-        vm[u] = live ? m[ch] : -INFINITY;
-        vl[u] = live ? l[ch] : 0.f;
+        vo[u] = o[(size_t)ch * D + dd];
+        vm[u] = m[ch];
+        vl[u] = l[ch];
+    }
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        const bool live = grp + u * G < n;
+        vo[u] = live ? vo[u] : 0.f;
+        vm[u] = live ? vm[u] : -INFINITY;
+        vl[u] = live ? vl[u] : 0.f;
     }
     float M = -INFINITY;
 #pragma unroll
