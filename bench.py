@@ -193,6 +193,42 @@ def pmc_case(torch, kv, q, att, dev):
     print(f"pmc case done: 24 decode launches, copy of {COPY_MIB} MiB", flush=True)
 
 
+def pmc_case_long(torch, kv_cls, dev, layers=4):
+    """configs[4]'s decode kernels for the --pmc runs: `layers` layers of 65536 positions
+    (each 537 MB of K+V, twice the Infinity Cache), one call per layer, then a plain copy
+    of known size that calibrates the byte counters."""
+    c = LONG
+    g = torch.Generator(device=dev)
+    g.manual_seed(c["seed"])
+    inv = inv_freq_torch(c["theta"], c["d"], dev)
+    kv = kv_cls(layers, c["L"], c["kv_heads"], c["d"])
+    kv.set_stream(torch.cuda.current_stream().cuda_stream)
+    pos = torch.arange(c["L"], device=dev)
+    for layer in range(layers):
+        k = rope_torch(torch.randn(c["L"], c["kv_heads"] * c["d"], generator=g, device=dev), c["kv_heads"], c["d"],
+                       pos, inv).contiguous()
+        v = torch.randn(c["L"], c["kv_heads"] * c["d"], generator=g, device=dev)
+        kv.append_device(layer, 0, c["L"], k.data_ptr(), v.data_ptr())
+        torch.cuda.synchronize()
+        del k, v
+    hd = c["heads"] * c["d"]
+    q = rope_torch(torch.randn(layers, hd, generator=g, device=dev), c["heads"], c["d"],
+                   torch.full((layers,), c["L"] - 1, device=dev), inv).contiguous()
+    att = torch.empty_like(q)
+    for layer in range(layers):
+        kv.attention_device(layer, c["heads"], q.data_ptr() + 4 * hd * layer, 1, c["L"] - 1,
+                            att.data_ptr() + 4 * hd * layer)
+    torch.cuda.synchronize()
+    grid = kv.last_grid()
+    kv.close()
+    src = torch.ones(COPY_MIB << 18, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"pmc case done: {layers} decode launches of configs[4] ({grid} workgroups), copy of {COPY_MIB} MiB",
+          flush=True)
+
+
 def cpu_baseline_decode(kv, q_host, threads, budget_s=12.0, max_reps=7):
     """wick's CPU attention (the oracle) on the host: decode over all 24 layers, median of reps."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -299,11 +335,56 @@ def measure_long_decode(torch, kv_cls, native, dev, steps):
     g32 = b32 / (ms32 * 1e-3) / 1e9
     at32 = {"L": L32, "workgroups": kv.last_grid(), "bytes_per_layer": b32, "us_per_layer": round(ms32 * 1e3, 2),
             "GBps": round(g32, 1), "pct_of_peak": round(100 * g32 / HBM_PEAK_GBS, 1)}
+    steps64 = measure_long_decode_steps(torch, kv, g, inv, dev)
     kv.close()
     best = sweep[0]
     return {"workload": "Llama-3-8B shape (Hq 32 / Hkv 8, d 128), 32 layers x 65536 positions (16 GiB K+V), "
                         "one query token per layer per step, eager launches",
-            "bytes_per_layer": bytes_layer, "auto": best, "chunk_sweep": sweep, "at_32k_context": at32}
+            "bytes_per_layer": bytes_layer, "auto": best, "chunk_sweep": sweep, "at_32k_context": at32,
+            "steps_64": steps64}
+
+
+def measure_long_decode_steps(torch, kv, g, inv, dev, nsteps=64):
+    """configs[4] as a decode loop (Session::step -> Model::forward, /root/reference/src/engine.rs:142-145,
+    src/model.rs:481-485): the cache holds 65536 - 64 positions; each of 64 steps appends the new
+    token's k and v rows (RoPE applied) at the next position of every layer and attends over the
+    grown cache, so the launch plan follows the length.  Timed with HIP events over all 64 x 32
+    (append, attention) pairs, eager launches on the bench stream."""
+    c = LONG
+    kvd, hd = c["kv_heads"] * c["d"], c["heads"] * c["d"]
+    base = c["L"] - nsteps
+    pos = torch.arange(base, c["L"], device=dev)
+    krows = rope_torch(torch.randn(nsteps, kvd, generator=g, device=dev), c["kv_heads"], c["d"], pos, inv).contiguous()
+    vrows = torch.randn(nsteps, kvd, generator=g, device=dev)
+    q = torch.randn(nsteps, c["layers"], hd, generator=g, device=dev)
+    q = rope_torch(q.view(nsteps * c["layers"], hd), c["heads"], c["d"], pos.repeat_interleave(c["layers"]),
+                   inv).view(nsteps, c["layers"], hd).contiguous()
+    att = torch.empty(c["layers"], hd, device=dev)
+
+    def run():
+        for s in range(nsteps):
+            kp, vp = krows[s].data_ptr(), vrows[s].data_ptr()
+            for layer in range(c["layers"]):
+                kv.append_device(layer, base + s, 1, kp, vp)
+                kv.attention_device(layer, c["heads"], q[s, layer].data_ptr(), 1, base + s,
+                                    att[layer].data_ptr())
+    run()  # warm-up: appending the same rows again rewrites the same bits
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    run()
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_time(e1)
+    pairs = nsteps * c["layers"]
+    attn_bytes = sum(decode_bytes(base + s + 1, c["heads"], c["kv_heads"], c["d"]) for s in range(nsteps)) * c["layers"]
+    append_bytes = pairs * 2 * 2 * kvd * 4  # k and v rows read and written
+    gbs = (attn_bytes + append_bytes) / (ms * 1e-3) / 1e9
+    return {"what": f"cache at {base} positions, then {nsteps} steps x {c['layers']} layers of (append one k/v row, "
+                    f"attention over {base + 1}..{c['L']} positions); eager launches",
+            "us_per_layer": round(ms * 1e3 / pairs, 2), "ms_per_step": round(ms / nsteps, 3),
+            "bytes": attn_bytes + append_bytes, "GBps": round(gbs, 1),
+            "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "workgroups_last_step": kv.last_grid()}
 
 
 def measure_e2e():
@@ -415,10 +496,11 @@ def main():
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--e2e-only", action="store_true", help="run only the e2e leg (configs[0]) and print its JSON")
     ap.add_argument("--no-long", action="store_true", help="skip configs[4] (16 GiB long-context decode)")
-    ap.add_argument("--pmc-case", nargs="?", const="decode", choices=["decode", "prefill"],
+    ap.add_argument("--pmc-case", nargs="?", const="decode", choices=["decode", "prefill", "prefill512", "long"],
                     help="short fixed workload for rocprofv3 --pmc runs: 'decode' = 24 decode calls (one per layer) "
-                         "and a 256 MiB device copy that calibrates the byte counters; 'prefill' = 3 launches of "
-                         "configs[2] at T=2048")
+                         "and a 256 MiB device copy that calibrates the byte counters; 'prefill' / 'prefill512' = "
+                         "3 launches of configs[2] at T=2048 / T=512; 'long' = configs[4]'s decode on 4 layers of "
+                         "65536 positions (537 MB of K+V each) and the calibrating copy")
     ap.add_argument("--decode-chunk", type=int, default=0)
     ap.add_argument("--no-ceiling", action="store_true", help="skip the read-ceiling / launch-floor probe")
     ap.add_argument("--eager", action="store_true", help="time eager launches only (no HIP graph)")
@@ -443,10 +525,14 @@ def main():
         print(json.dumps(measure_e2e()), flush=True)
         return
 
-    if args.pmc_case == "prefill":
-        measure_prefill(torch, DeviceKvCache, dev, PRE["heads"], PRE["kv_heads"], PRE["d"], PRE["T"], 0,
+    if args.pmc_case in ("prefill", "prefill512"):
+        T = PRE["T"] if args.pmc_case == "prefill" else 512
+        measure_prefill(torch, DeviceKvCache, dev, PRE["heads"], PRE["kv_heads"], PRE["d"], T, 0,
                         PRE["theta"], PRE["seed"], qk_norm=True, steps=3)
-        print("pmc case done: prefill T=2048", flush=True)
+        print(f"pmc case done: prefill T={T}", flush=True)
+        return
+    if args.pmc_case == "long":
+        pmc_case_long(torch, DeviceKvCache, dev)
         return
 
     # ---------------- decode (the headline)

@@ -61,6 +61,50 @@ def test_decode_llama3_8b_shape_65536():
     check(q, k, v, 1, 65535, 32, 8, 128)
 
 
+def test_long_decode_steps_append_llama3_8b_shape():
+    """configs[4] as a decode loop (Session::step -> Model::forward,
+    /root/reference/src/engine.rs:142-145, src/model.rs:481-485): the cache holds
+    65472 positions, then 64 steps each append the token's k/v row at the next
+    position of every layer and attend over the grown cache, up to 65536.  The
+    appended rows read back bit-exact; the first and the last step's outputs
+    (65473 and 65536 positions) match the oracle.  Two layers of the config's
+    per-layer shape (Hq 32 / Hkv 8, d 128, 512 MiB of K+V each) keep the host
+    copy small."""
+    heads, kvh, d, L, nsteps, layers = 32, 8, 128, 65536, 64, 2
+    base = L - nsteps
+    inv = inv_freq(500000.0, d)
+    rng = np.random.default_rng(5)
+    ks, vs, qs = [], [], []
+    for layer in range(layers):
+        k = rope_np(rng.standard_normal((L, kvh * d), dtype=np.float32), kvh, d, np.arange(L), inv)
+        ks.append(k)
+        vs.append(rng.standard_normal((L, kvh * d), dtype=np.float32))
+        qs.append(rope_np(rng.standard_normal((nsteps, heads * d), dtype=np.float32), heads, d,
+                          np.arange(base, L), inv))
+    outs = {}
+    with DeviceKvCache(layers, L, kvh, d) as kv:
+        for layer in range(layers):
+            kv.append(layer, 0, ks[layer][:base], vs[layer][:base])
+        grids = []
+        for s in range(nsteps):
+            for layer in range(layers):
+                kv.append(layer, base + s, ks[layer][base + s:base + s + 1], vs[layer][base + s:base + s + 1])
+                att = kv.attention(layer, heads, qs[layer][s:s + 1], base + s)
+                if s in (0, nsteps - 1):
+                    outs[(layer, s)] = att
+            grids.append(kv.last_grid())
+        for layer in range(layers):
+            kr, vr = kv.read(layer, base, nsteps)
+            assert np.array_equal(kr, ks[layer][base:]) and np.array_equal(vr, vs[layer][base:]), layer
+    print(f"decode grids over the 64 steps: {sorted(set(grids))}")
+    for (layer, s), got in outs.items():
+        n = base + s + 1
+        want = ol.attention(qs[layer][s:s + 1], ks[layer][:n], vs[layer][:n], 1, base + s, heads, kvh, d)
+        ok, mabs, mrel = within_tol(got, want)
+        print(f"layer {layer} step {s} ({n} positions): max abs {mabs:.2e} max rel {mrel:.2e}")
+        assert ok, (layer, s, mabs, mrel)
+
+
 @pytest.mark.parametrize("L", [1, 2, 15, 16, 17, 63, 64, 65, 129, 1000, 4097])
 @pytest.mark.parametrize("d", [16, 32, 64, 128])
 def test_decode_lengths_and_head_dims(L, d):
