@@ -125,3 +125,35 @@ def test_smollm2_135m_attention_teacher_forced():
             got = kv.attention(layer, cfg.heads, qt[layer], 0)
             ok, mabs, mrel = within_tol(got, at[layer])
             assert ok, f"layer {layer}: max abs {mabs:.3e} max rel {mrel:.3e}"
+
+
+def test_smollm2_135m_decode_attention_teacher_forced():
+    """Per-layer attention at every one of the 64 greedy decode steps of configs[0]
+    (the call site src/model.rs:485 with t = 1 at positions 128..191), both sides fed
+    the CPU run's q and K/V: the step's new k/v row is appended to the device cache
+    from the oracle's cache and the device attention must match the oracle's output
+    for that layer within 2e-5 + 1e-4*|ref|.  The cache rows read back bit-exact."""
+    cfg = smollm2_135m()
+    w = random_weights(cfg, seed=0)
+    prompt = random_prompt(1, 128, cfg.vocab)
+    om = ol.OracleModel(cfg, w)
+    st = om.new_state(256)
+    logits = om.forward(st, prompt)
+    worst_abs, worst_rel = 0.0, 0.0
+    with DeviceKvCache(cfg.layers, 256, cfg.kv_heads, cfg.head_dim) as kv:
+        for layer in range(cfg.layers):
+            kv.append(layer, 0, st["k"][layer, :128], st["v"][layer, :128])
+        for s in range(64):
+            tok = ol.argmax(logits[0])
+            pos = 128 + s
+            logits, qt, at = om.forward(st, [tok], trace=True)
+            for layer in range(cfg.layers):
+                kv.append(layer, pos, st["k"][layer, pos:pos + 1], st["v"][layer, pos:pos + 1])
+                got = kv.attention(layer, cfg.heads, qt[layer], pos)
+                ok, mabs, mrel = within_tol(got, at[layer])
+                worst_abs, worst_rel = max(worst_abs, mabs), max(worst_rel, mrel)
+                assert ok, f"step {s} layer {layer}: max abs {mabs:.3e} max rel {mrel:.3e}"
+        for layer in (0, cfg.layers - 1):
+            kr, vr = kv.read(layer, 0, 192)
+            assert np.array_equal(kr, st["k"][layer, :192]) and np.array_equal(vr, st["v"][layer, :192])
+    print(f"64 steps x {cfg.layers} layers: max abs {worst_abs:.2e}, max rel {worst_rel:.2e}")
