@@ -183,6 +183,57 @@ def test_decode_matches_step_by_step_forward():
     assert again == chain[:1]
 
 
+def _bias_and_norms(cfg, w, seed):
+    """Give every layer q/k/v biases and QK-norm weights (Qwen2's and Qwen3's extra tensors)."""
+    rng = np.random.default_rng(seed)
+    r = lambda n, s=0.1, c=0.0: (c + s * rng.standard_normal(n)).astype(np.float32)  # noqa: E731
+    for lw in w["layers"]:
+        lw.update(bq=r(cfg.q_dim), bk=r(cfg.kv_dim), bv=r(cfg.kv_dim), q_norm=r(cfg.head_dim, 0.1, 1.0),
+                  k_norm=r(cfg.head_dim, 0.1, 1.0))
+    return w
+
+
+def _replay_case(name):
+    if name in MODELS:
+        cfg, w, _ = fixture(name)
+        return cfg, w
+    if name == "group18-d64-bias-qknorm":
+        cfg = Config("qwen3", 128, 256, 2, 36, 2, 64, 512, rms_eps=1e-6, rope_theta=1e6, attn_bias=True, qk_norm=True)
+        return cfg, _bias_and_norms(cfg, random_weights(cfg, seed=21, std=0.05), 22)
+    cfg = Config("llama", 256, 512, 2, 8, 2, 128, 512, rms_eps=1e-5, rope_theta=500000.0)
+    return cfg, random_weights(cfg, seed=23, std=0.05)
+
+
+@pytest.mark.parametrize("name", ["qwen2-bias-bf16", "qwen3-qknorm-f32", "llama3-scaled-f32",
+                                  "group18-d64-bias-qknorm", "d128-group4"])
+def test_decode_replay_matches_step_by_step(name):
+    """64 decode steps at 65..128 positions share one decode plan, so decode() launches the
+    first and replays the other 63 from a captured HIP graph: head_dim 16 with biases, 32 with
+    QK-norm, a group of 18 (two 16-head slices writing the same k/v rows) with both, and
+    head_dim 128.  The ids and every layer's cache bits must equal forward() + host argmax
+    launched step by step."""
+    cfg, w = _replay_case(name)
+    prompt = random_prompt(9, 64, cfg.vocab)
+    n = 64
+    with DeviceModel(cfg, w) as m:
+        c1 = m.new_cache(160)
+        first = m.prefill(c1, prompt)
+        chain = m.decode(c1, first, n)
+        c2 = m.new_cache(160)
+        logits = m.forward(c2, prompt)
+        assert int(np.argmax(logits[0])) == first
+        tok, steps = first, []
+        for _ in range(n):
+            logits = m.forward(c2, [tok])
+            tok = ol.argmax(logits[0])
+            steps.append(tok)
+        for layer in range(cfg.layers):
+            k1, v1 = c1.read(layer, 0, 64 + n)
+            k2, v2 = c2.read(layer, 0, 64 + n)
+            assert np.array_equal(k1, k2) and np.array_equal(v1, v2), f"{name}: layer {layer} cache differs"
+    assert chain == steps
+
+
 def test_prefill_chunks_of_256():
     """A 300-token prompt runs as chunks of 256 + 44 (src/engine.rs:107, :134)."""
     cfg, w, exp = fixture("qwen3-qknorm-f32")

@@ -278,9 +278,12 @@ int upload_ids(wick_hip_model *m, const uint32_t *ids, int n) {
     return WICK_HIP_OK;
 }
 
-// Shortest run of equal-plan decode steps worth a capture: below it the
-// steps launch directly (capture and instantiation cost about as much as
-// ~20 steps' worth of launch gaps save).
+// Fewest steps worth replaying from a captured graph.  A run of equal-plan
+// steps launches its first step directly (it makes any allocation the step
+// needs, and the capture is taken from the same launch code); the remaining
+// steps are replayed when there are at least this many of them, else they
+// launch directly too (capture and instantiation cost about as much as ~20
+// steps' worth of launch gaps save).
 constexpr int kGraphMinSteps = 24;
 
 // Greedy step i of a decode loop, launched directly: forward of ids[i] at
@@ -509,7 +512,7 @@ int wick_hip_model_decode(wick_hip_model *m, wick_hip_kv *kv, uint32_t first, in
         int j = i + 1;
         while (j < steps && wick::decode_plan_key(kv, m->c.heads, start + j + 1) == plan) j++;
         RC_TRY(decode_step(m, kv, start, i));
-        if (j - i > kGraphMinSteps) {
+        if (j - (i + 1) >= kGraphMinSteps) {
             RC_TRY(decode_replayed(m, kv, start, i + 1, j));
         } else {
             for (int k = i + 1; k < j; k++) RC_TRY(decode_step(m, kv, start, k));
