@@ -361,6 +361,50 @@ int attend_model(wick_hip_kv *kv, int layer, int heads, float *q_dev, const floa
     return run_attention(kv, layer, heads, q_dev, t, start, att_dev);
 }
 
+int attend_model_oproj(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev, const float *v_dev,
+                       int start, const float *wo, int hidden, float *oparts, int *units_out, const int *len_dev) {
+    int rc = check_kv(kv, layer);
+    if (rc) return rc;
+    if ((rc = check_span(kv, start, 1))) return rc;
+    if (!q_dev || !k_dev || !v_dev || !wo || !oparts || !units_out) return fail(WICK_HIP_EINVAL, "null argument");
+    if ((rc = check_aligned(q_dev, "q_dev")) || (rc = check_aligned(k_dev, "k_dev")) ||
+        (rc = check_aligned(v_dev, "v_dev")))
+        return rc;
+    if (heads < 1 || heads % kv->kv_heads != 0)
+        return fail(WICK_HIP_EINVAL, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv->kv_heads);
+    if (hidden < 1) return fail(WICK_HIP_EINVAL, "hidden must be >= 1");
+    const int group = heads / kv->kv_heads;
+    const int hslices = (group + wick::kTileRows - 1) / wick::kTileRows;
+    int chunk, nchunks;
+    plan_chunks(kv, kv->kv_heads * hslices, start + 1, &chunk, &nchunks);
+    if (!wick::decode_oproj_supported(kv->head_dim, group, nchunks)) return 1;
+    PrepConsts c;
+    if ((rc = prep_consts(kv, layer, heads, &c))) return rc;
+    wick::DecodeArgs a{};
+    if ((rc = plan_decode(kv, layer, group, start + 1, q_dev, nullptr, &a))) return rc;
+    a.scale = 1.0f / sqrtf((float)kv->head_dim);  // src/model.rs:527
+    a.prep = 1;
+    a.kraw = k_dev;
+    a.vraw = v_dev;
+    a.bq = c.bq;
+    a.bk = c.bk;
+    a.bv = c.bv;
+    a.qn = c.qn;
+    a.kn = c.kn;
+    a.rope_cos = kv->rope_cos;
+    a.rope_sin = kv->rope_sin;
+    a.eps = c.eps;
+    a.len_dev = len_dev;
+    a.wo = wo;
+    a.oparts = oparts;
+    a.hidden = hidden;
+    a.wo_ld = heads * kv->head_dim;
+    hipError_t e = wick::launch_decode_oproj(kv->head_dim, a, kv->stream);
+    if (e != hipSuccess) return hip_fail(e, "decode + output projection launch");
+    *units_out = kv->kv_heads * hslices;
+    return WICK_HIP_OK;
+}
+
 long long decode_plan_key(const wick_hip_kv *kv, int heads, int len) {
     const int group = heads / kv->kv_heads;
     const int hslices = (group + wick::kTileRows - 1) / wick::kTileRows;

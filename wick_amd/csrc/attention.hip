@@ -31,6 +31,7 @@
 //       dmap(row, db) = 64*(db/4) + W*row + db%4 (W = min(D/16, 4)), so lane
 //       (i, g) loads V[p0+4g+m][64*seg + W*i .. +W) as one W-vector.
 #include "attn_kernels.h"
+#include "wave_ops.h"
 
 #include <math.h>
 
@@ -610,16 +611,22 @@ struct DecodeSpace {
 // or two tile groups instead of two to four.
 // TG: 16-key tiles per softmax group of the lean core (head_dim 64 and 128);
 // one tile per group halves the products a wave runs after its last load.
-template <int D, bool PREP, bool PP = (D < 128), int NW = 4, int TG = Shape<D>::TG>
+// OPROJ: one chunk per unit and the output projection fused in (DecodeArgs'
+// wo / oparts): workgroup (unit, row block) requests its rows of wo first,
+// computes the unit's attention (every row block of a unit repeats it; each
+// writes the same prepared k/v bits), keeps the normalised output in LDS and
+// writes the unit's partial product for its rows.
+template <int D, bool PREP, bool PP = (D < 128), int NW = 4, int TG = Shape<D>::TG, bool OPROJ = false>
 __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
     using S = Shape<D>;
     __shared__ float sm_m[NW][16], sm_l[NW][16];
     __shared__ __attribute__((aligned(16))) float sm_o[NW][16][D];
     __shared__ float sq[PREP ? 16 : 1][D];  // prepared q rows (PREP)
+    __shared__ float satt[OPROJ ? 16 * D : 1];  // normalised output of the unit's heads (OPROJ)
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int units = a.kv_heads * a.hslices;
-    const int unit = blockIdx.x % units, chunk = blockIdx.x / units;
+    const int unit = blockIdx.x % units, chunk = OPROJ ? 0 : blockIdx.x / units;
     const int kvh = unit / a.hslices, slice = unit % a.hslices;
     const int col0 = slice * 16, ncols = min(16, a.group - col0);
     const int head0 = kvh * a.group + col0;
@@ -628,6 +635,25 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
     // the cache length: the argument, or (graph-replayed decode loop) a device counter
     const int len = a.len_dev ? *a.len_dev : a.len;
     const int kbeg = chunk * a.chunk, kend = min(kbeg + a.chunk, len);
+
+    // OPROJ: this wave's kOprojRows rows of wo over the unit's ncols*D
+    // columns, requested before anything waits on memory: lane l holds column
+    // 64*j + l of row orow0 + r at wreg[r][j].
+    float wreg[OPROJ ? kOprojRows : 1][OPROJ ? kOprojChunks : 1];
+    int orow0 = 0, onrows = 0, cw = 0;
+    if constexpr (OPROJ) {
+        const int rblk = blockIdx.x / units;
+        const int bend = min(a.hidden, (rblk + 1) * NW * kOprojRows);
+        orow0 = rblk * NW * kOprojRows + w * kOprojRows;
+        onrows = max(0, min(kOprojRows, bend - orow0));
+        cw = ncols * D / 64;
+        const float *wr = a.wo + (size_t)head0 * D + lane;
+#pragma unroll
+        for (int r = 0; r < kOprojRows; r++)
+#pragma unroll
+            for (int j = 0; j < kOprojChunks; j++)
+                wreg[r][j] = (r < onrows && j < cw) ? wr[(size_t)(orow0 + r) * a.wo_ld + 64 * j] : 0.f;
+    }
 
     const int col = lane & 15, g = lane >> 4;
     f4 q[S::KJ];
@@ -752,7 +778,28 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
                 o += sm_o[ww][c][d] * e;
                 L += sm_l[ww][c] * e;
             }
-            a.att[(size_t)(head0 + c) * D + d] = o / L;
+            if constexpr (OPROJ)
+                satt[idx] = o / L;
+            else
+                a.att[(size_t)(head0 + c) * D + d] = o / L;
+        }
+        if constexpr (OPROJ) {
+            // partial output projection of this wave's rows: the lane's
+            // columns in order, then a fixed butterfly
+            __syncthreads();
+            float sum[kOprojRows];
+#pragma unroll
+            for (int r = 0; r < kOprojRows; r++) {
+                sum[r] = 0.f;
+#pragma unroll
+                for (int j = 0; j < kOprojChunks; j++)
+                    if (j < cw) sum[r] = fmaf(wreg[r][j], satt[64 * j + lane], sum[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < kOprojRows; r++) {
+                sum[r] = wave_sum(sum[r]);
+                if (lane == 0 && r < onrows) a.oparts[(size_t)unit * a.hidden + orow0 + r] = sum[r];
+            }
         }
     } else {
         // 4 consecutive dims of one column per thread, which works out that
@@ -1298,6 +1345,26 @@ hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_
     if (e != hipSuccess || a.nchunks == 1) return e;
     const int slices = head_dim / 16;
     WICK_DISPATCH_D(head_dim, decode_merge_kernel, dim3(a.kv_heads * a.group * slices), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+bool decode_oproj_supported(int head_dim, int group, int nchunks) {
+    if (nchunks != 1 || (head_dim != 64 && head_dim != 128)) return false;
+    const int ncols = group < kTileRows ? group : kTileRows;
+    return ncols * head_dim <= 64 * kOprojChunks;
+}
+
+hipError_t launch_decode_oproj(int head_dim, DecodeArgs a, hipStream_t s) {
+    // each wave of a workgroup takes at most one group of tiles (chunk <= 8
+    // waves x 32 keys at head_dim 64; head_dim 128 loops over 16-key groups)
+    if (!a.prep || !decode_oproj_supported(head_dim, a.group, a.nchunks) || a.chunk > 8 * 2 * 16)
+        return hipErrorInvalidValue;
+    const int blocks = (a.hidden + 8 * kOprojRows - 1) / (8 * kOprojRows);
+    const dim3 grid((unsigned)(a.kv_heads * a.hslices * blocks));
+    if (head_dim == 64)
+        hipLaunchKernelGGL((decode_kernel<64, true, false, 8, 2, true>), grid, dim3(512), 0, s, a);
+    else
+        hipLaunchKernelGGL((decode_kernel<128, true, false, 8, 1, true>), grid, dim3(512), 0, s, a);
     return hipGetLastError();
 }
 

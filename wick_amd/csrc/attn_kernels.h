@@ -37,7 +37,20 @@ struct DecodeArgs {
     // HIP graph replays one decode step for successive lengths); chunk and
     // nchunks must then suit every length it takes: plan_decode's plan for it.
     const int *len_dev;
+    // Fused output projection (launch_decode_oproj; one chunk per unit): the
+    // grid is units x row blocks of 8 * kOprojRows rows; workgroup (unit, b)
+    // multiplies the unit's attention output by its rows of wo ([hidden]
+    // [wo_ld], wick's o_proj layout) restricted to the unit's columns, and
+    // writes that partial product to oparts[unit][row].  att is not written.
+    const float *wo;
+    float *oparts;
+    int hidden, wo_ld;
 };
+
+// Fused output projection: rows per wave, and the most 64-column chunks of a
+// unit's output (ncols * head_dim <= 64 * kOprojChunks).
+constexpr int kOprojRows = 4;
+constexpr int kOprojChunks = 4;
 
 struct PrefillArgs {
     const float *q;   // [t][heads*D]
@@ -89,6 +102,12 @@ bool prefill_has_rows32(int head_dim, int capacity, int split);
 
 // Launches decode_kernel and, when it splits the keys, decode_merge_kernel.
 hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_t s);
+// Whether decode_kernel's fused output projection serves this shape (head_dim
+// 64 or 128, one chunk per unit, the unit's columns fit kOprojChunks).
+bool decode_oproj_supported(int head_dim, int group, int nchunks);
+// The fused decode + partial output projection (a.prep set, a.nchunks == 1):
+// units x ceil(hidden / (8 kOprojRows)) workgroups of 8 waves.
+hipError_t launch_decode_oproj(int head_dim, DecodeArgs a, hipStream_t s);
 int prefill_grid(int head_dim, const PrefillArgs &a);
 hipError_t launch_prefill(int head_dim, const PrefillArgs &a, hipStream_t s);
 hipError_t launch_append(int head_dim, const AppendArgs &a, hipStream_t s);
@@ -110,6 +129,16 @@ bool kv_info(const wick_hip_kv *kv, KvInfo *out);
 // launch plan, which decode_plan_key identifies.
 int attend_model(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev, const float *v_dev, int t,
                  int start, float *att_dev, const int *len_dev = nullptr);
+
+// attend_model for one token with the output projection fused in: oparts
+// [units][hidden] receives each (kv head, 16-head slice) unit's partial
+// product wo[:, unit's columns] . att[unit's columns]; their sum in unit order
+// is wo . att.  Returns WICK_HIP_OK, or 1 (nothing launched) when the fused
+// form does not serve this shape -- the caller then uses attend_model and a
+// separate product.  *units_out: the number of partial vectors.
+int attend_model_oproj(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev, const float *v_dev,
+                       int start, const float *wo, int hidden, float *oparts, int *units_out,
+                       const int *len_dev = nullptr);
 
 // The decode launch plan (chunk size and count) for `heads` query heads over
 // len cached positions: equal keys launch the same kernels on the same grids.

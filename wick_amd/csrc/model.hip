@@ -14,18 +14,13 @@
 #include <math.h>
 
 #include "model_kernels.h"
+#include "wave_ops.h"
 
 namespace wick {
 
 namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
 
 __device__ __forceinline__ float dot4(const f4 w, const f4 x, float acc) {
     acc = fmaf(w.x, x.x, acc);
@@ -79,9 +74,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
         for (int r = 0; r < R; r++) wv[r][u] = c < C4 ? __builtin_nontemporal_load(W[r] + c) : zero;
         if (EPI == kEpiSwiglu) wv2[u] = c < C4 ? __builtin_nontemporal_load(W2 + c) : zero;
     }
-    // the value the residual epilogue adds to (lane tk: token tk)
-    float resid = 0.0f;
-    if (EPI == kEpiResid && lane < nt) resid = a.out0[(size_t)(tok0 + lane) * a.ld0 + row0];
+    // the values the residual epilogue adds to (lane tk: token tk, one per row)
+    float resid[EPI == kEpiResid ? R : 1];
+    if constexpr (EPI == kEpiResid) {
+        const float *src = a.resid ? a.resid : a.out0;
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            resid[r] = (lane < nt && row0 + r < a.rows) ? src[(size_t)(tok0 + lane) * a.ld0 + row0 + r] : 0.0f;
+    }
 
     // rmsnorm (src/kernels.rs:343-349) of each input row: xn = x * scale * g
     float scale[NT];
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
             if (EPI == kEpiStore || EPI == kEpiArgmax) {
                 a.out0[tok * a.ld0 + row] = d;
             } else if (EPI == kEpiResid) {
-                a.out0[tok * a.ld0 + row] = resid + d;
+                a.out0[tok * a.ld0 + row] = resid[r] + d;
             } else if (EPI == kEpiQkv) {
                 if (row < a.split0)
                     a.out0[tok * a.ld0 + row] = d;
@@ -178,6 +178,83 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
                 if (row0 + r < a.rows) arg_better(acc[r][0], row0 + r, bv, bi);
             reinterpret_cast<float2 *>(a.out1)[row0 / R] = make_float2(bv, __int_as_float(bi));
         }
+    }
+}
+
+// The gate/up product of one token after the fused decode + output
+// projection: the input row is x + parts[0] + ... + parts[nparts-1] (the
+// units' partial products of wo . att, added in unit order: the residual add
+// of src/model.rs:486-487), RMSNorm'ed (ffn_norm), then silu(gate) * up
+// (src/model.rs:490-501).  One wave per output row, the whole row in one pass
+// (cols <= 64 * UNR float4s): every load -- both weight rows, x, the partial
+// vectors, the norm weight -- is issued before the first use, so the kernel
+// waits for memory once.  The wave of row 0 writes the summed row to xout (the
+// residual the down product adds to).
+template <int UNR, int NP, int R>
+__global__ __launch_bounds__(256) void gemv_swiglu_parts_kernel(const GemvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+    if (row0 >= a.rows) return;  // whole waves only; no barriers below
+    const int C4 = a.cols >> 2;
+    const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    const f4 *X = reinterpret_cast<const f4 *>(a.x);
+    const f4 *G = reinterpret_cast<const f4 *>(a.norm);
+    f4 wg[R][UNR], wu[R][UNR], xv[UNR], gv[UNR], pv[NP][UNR];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int row = min(row0 + r, a.rows - 1);
+        const f4 *Wg = reinterpret_cast<const f4 *>(a.w + (size_t)row * a.cols);
+        const f4 *Wu = reinterpret_cast<const f4 *>(a.w2 + (size_t)row * a.cols);
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int c = lane + 64 * u;
+            wg[r][u] = c < C4 ? __builtin_nontemporal_load(Wg + c) : zero;
+            wu[r][u] = c < C4 ? __builtin_nontemporal_load(Wu + c) : zero;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; u++) {
+        const int c = lane + 64 * u;
+        xv[u] = c < C4 ? X[c] : zero;
+        gv[u] = c < C4 ? G[c] : zero;
+#pragma unroll
+        for (int p = 0; p < NP; p++)
+            pv[p][u] = (p < a.nparts && c < C4) ? reinterpret_cast<const f4 *>(a.parts + (size_t)p * a.cols)[c] : zero;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < UNR; u++) {
+#pragma unroll
+        for (int p = 0; p < NP; p++)
+            if (p < a.nparts) xv[u] += pv[p][u];
+        ss = dot4(xv[u], xv[u], ss);
+    }
+    if (row0 == 0) {
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int c = lane + 64 * u;
+            if (c < C4) reinterpret_cast<f4 *>(a.xout)[c] = xv[u];
+        }
+    }
+    ss = wave_sum(ss);
+    const float scale = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+    float acc[R], acc2[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = acc2[r] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < UNR; u++) {
+        const f4 x = xv[u] * scale * gv[u];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            acc[r] = dot4(wg[r][u], x, acc[r]);
+            acc2[r] = dot4(wu[r][u], x, acc2[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        acc[r] = wave_sum(acc[r]);
+        acc2[r] = wave_sum(acc2[r]);
+        if (lane == 0 && row0 + r < a.rows) a.out0[row0 + r] = acc[r] / (1.0f + expf(-acc[r])) * acc2[r];
     }
 }
 
@@ -371,11 +448,23 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
         }
         for (int i = 4 * n4 + threadIdx.x; i < n; i += 1024) arg_better(x[i], i, bv, bi);
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(bv, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        arg_better(ov, oi, bv, bi);
+    // the wave's best pair on lane moves (no lane holds a NaN as its best, so
+    // "better of two" is commutative and every lane ends with the wave's best)
+    arg_better(dpp_f<kDppQuadXor1>(bv), dpp_i<kDppQuadXor1>(bi), bv, bi);
+    arg_better(dpp_f<kDppQuadXor2>(bv), dpp_i<kDppQuadXor2>(bi), bv, bi);
+    arg_better(dpp_f<kDppRowHalfMirror>(bv), dpp_i<kDppRowHalfMirror>(bi), bv, bi);
+    arg_better(dpp_f<kDppRowMirror>(bv), dpp_i<kDppRowMirror>(bi), bv, bi);
+    {
+        const auto pv = __builtin_amdgcn_permlane16_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
+        const auto pi = __builtin_amdgcn_permlane16_swap((unsigned)bi, (unsigned)bi, false, false);
+        arg_better(__uint_as_float(pv[0]), (int)pi[0], bv, bi);
+        arg_better(__uint_as_float(pv[1]), (int)pi[1], bv, bi);
+    }
+    {
+        const auto pv = __builtin_amdgcn_permlane32_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
+        const auto pi = __builtin_amdgcn_permlane32_swap((unsigned)bi, (unsigned)bi, false, false);
+        arg_better(__uint_as_float(pv[0]), (int)pi[0], bv, bi);
+        arg_better(__uint_as_float(pv[1]), (int)pi[1], bv, bi);
     }
     const int w = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
@@ -432,6 +521,17 @@ hipError_t gemv_epi(const GemvArgs &a, hipStream_t s) {
 
 hipError_t launch_gemv(int epi, const GemvArgs &a, hipStream_t s) {
     if (a.rows <= 0 || a.t <= 0) return hipSuccess;
+    if (a.parts) {
+        // the gate/up product after the fused decode + output projection
+        if (epi != kEpiSwiglu || a.t != 1 || !a.norm || !a.xout || a.nparts < 1 || a.nparts > kMaxParts ||
+            a.cols > 4 * 64 * 4)
+            return hipErrorInvalidValue;
+        // one row per wave: more waves in flight beat sharing the input row
+        // (2 rows per wave measured 4% slower end to end, 4 rows 14%)
+        const dim3 grid((unsigned)((a.rows + 3) / 4)), block(256);
+        hipLaunchKernelGGL((gemv_swiglu_parts_kernel<4, kMaxParts, 1>), grid, block, 0, s, a);
+        return hipGetLastError();
+    }
     switch (epi) {
     case kEpiStore: return gemv_epi<kEpiStore>(a, s);
     case kEpiResid: return gemv_epi<kEpiResid>(a, s);

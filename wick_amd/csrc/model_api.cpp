@@ -9,6 +9,10 @@
 //   gemv  wo, residual add into x                      (:486-487)
 //   gemv  ffn_norm + w_gate, w_up, silu_mul -> h       (:490-501)
 //   gemv  w_down, residual add into x                  (:502-503)
+// For one token over a short cache (one decode chunk per unit, head_dim 64 or
+// 128, small GQA groups) the attention and the wo product are one launch that
+// writes each unit's partial product, and the gate/up product adds those to
+// the residual as its prologue: four launches per layer instead of five.
 // then the final norm + LM head (:507-515) and, for the greedy entry points,
 // sampler::argmax (src/sampler.rs:129-137), all on the model's stream.
 #include "wick_hip_model.h"
@@ -70,6 +74,9 @@ struct wick_hip_model {
     // activations, sized for `cap_t` tokens
     int cap_t = 0;
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *h = nullptr;
+    // one token with the output projection fused into the decode kernel: the
+    // per-unit partial products [units][hidden] and the residual after them
+    float *oparts = nullptr, *xr = nullptr;
     int cap_logits = 0;  // rows of logits
     float *logits = nullptr;
     float *argparts = nullptr;  // the LM head's argmax pairs for the last token (argmax_parts(vocab) of them)
@@ -92,10 +99,10 @@ int upload(wick_hip_model *m, float **dst, const float *src, size_t n, const cha
 }
 
 void free_activations(wick_hip_model *m) {
-    void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->att, m->h};
+    void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->att, m->h, m->oparts, m->xr};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
-    m->x = m->xn = m->q = m->k = m->v = m->att = m->h = nullptr;
+    m->x = m->xn = m->q = m->k = m->v = m->att = m->h = m->oparts = m->xr = nullptr;
     m->cap_t = 0;
 }
 
@@ -112,6 +119,19 @@ int ensure_activations(wick_hip_model *m, int t) {
                 {&m->h, (size_t)c.intermediate}};
     for (auto &w : want) {
         hipError_t e = hipMalloc(w.p, (size_t)t * w.n * sizeof(float));
+        if (e != hipSuccess) {
+            free_activations(m);
+            return hip_fail(e, "hipMalloc(activations)");
+        }
+    }
+    const int group = c.heads / c.kv_heads;
+    const size_t units = (size_t)c.kv_heads * ((group + wick::kTileRows - 1) / wick::kTileRows);
+    struct {
+        float **p;
+        size_t n;
+    } one[] = {{&m->oparts, units * c.hidden}, {&m->xr, (size_t)c.hidden}};
+    for (auto &w : one) {
+        hipError_t e = hipMalloc(w.p, w.n * sizeof(float));
         if (e != hipSuccess) {
             free_activations(m);
             return hip_fail(e, "hipMalloc(activations)");
@@ -197,6 +217,11 @@ int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, 
     RC_TRY(ensure_logits(m, all_logits ? t : 1));
     hipError_t e = wick::launch_embed(m->embed, tok_dev, m->x, t, c.hidden, s, counters);
     if (e != hipSuccess) return hip_fail(e, "embed kernel launch");
+    // the gate/up product takes at most kMaxParts partial vectors of up to
+    // 1024 floats (one pass of its waves)
+    const int group = c.heads / c.kv_heads;
+    const bool fusable = t == 1 && c.kv_heads * ((group + wick::kTileRows - 1) / wick::kTileRows) <= wick::kMaxParts &&
+                         c.hidden <= 1024;
     for (int li = 0; li < c.layers; li++) {
         const wick_hip_model::Layer &L = m->layers[li];
         wick::GemvArgs g{};
@@ -215,6 +240,44 @@ int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, 
         g.cols = c.hidden;
         g.t = t;
         RC_TRY(product(m, wick::kEpiQkv, g, "qkv product launch"));
+
+        // One token: attention and the output projection in one launch
+        // (per-unit partial products), added to the residual by the gate/up
+        // product's prologue; the down product then adds to that sum.
+        int units = 0;
+        const int fused = fusable ? wick::attend_model_oproj(kv, li, c.heads, m->q, m->k, m->v, start, L.wo, c.hidden,
+                                                             m->oparts, &units, counters ? counters + 1 : nullptr)
+                                  : 1;
+        if (fused < 0) return fused;
+        if (fused == 0) {
+            g = wick::GemvArgs{};
+            g.x = m->x;
+            g.parts = m->oparts;
+            g.nparts = units;
+            g.xout = m->xr;
+            g.norm = L.ffn_norm;
+            g.eps = c.rms_eps;
+            g.w = L.w_gate;
+            g.w2 = L.w_up;
+            g.out0 = m->h;
+            g.ld0 = c.intermediate;
+            g.rows = c.intermediate;
+            g.cols = c.hidden;
+            g.t = 1;
+            RC_TRY(product(m, wick::kEpiSwiglu, g, "residual + gate/up product launch"));
+
+            g = wick::GemvArgs{};
+            g.x = m->h;
+            g.w = L.w_down;
+            g.resid = m->xr;
+            g.out0 = m->x;
+            g.ld0 = c.hidden;
+            g.rows = c.hidden;
+            g.cols = c.intermediate;
+            g.t = 1;
+            RC_TRY(product(m, wick::kEpiResid, g, "down product launch"));
+            continue;
+        }
 
         RC_TRY(wick::attend_model(kv, li, c.heads, m->q, m->k, m->v, t, start, m->att, counters ? counters + 1 : nullptr));
 

@@ -18,6 +18,9 @@ enum GemvEpilogue {
                      // (value, index) pair per kArgmaxRows rows, see launch_argmax
 };
 
+// Most partial vectors the gate/up product adds to its input row.
+constexpr int kMaxParts = 4;
+
 // Logit rows per argmax partial (the LM head's rows per wave).
 constexpr int kArgmaxRows = 4;
 __host__ __device__ inline int argmax_parts(int rows) { return (rows + kArgmaxRows - 1) / kArgmaxRows; }
@@ -32,6 +35,15 @@ struct GemvArgs {
     int split0, split1;   // kEpiQkv: rows [0,split0) -> out0, [split0,split1) -> out1, the rest -> out2
     int rows, cols, t;
     float eps;
+    // kEpiSwiglu, one token, cols <= 1024: the input row is x + parts[0] + ...
+    // + parts[nparts-1] (nparts <= kMaxParts partial vectors of cols floats,
+    // added in that order: the fused decode's per-unit output projections);
+    // the wave of row 0 also writes that sum to xout.  Null parts: x as is.
+    const float *parts;
+    int nparts;
+    float *xout;
+    // kEpiResid: the value added to, resid[tok][row] (stride ld0); null: out0 itself
+    const float *resid;
 };
 
 // out rows of a matrix-vector (or small matrix-matrix) product with the
