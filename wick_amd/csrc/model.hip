@@ -181,80 +181,142 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
     }
 }
 
-// The gate/up product of one token after the fused decode + output
-// projection: the input row is x + parts[0] + ... + parts[nparts-1] (the
-// units' partial products of wo . att, added in unit order: the residual add
-// of src/model.rs:486-487), RMSNorm'ed (ffn_norm), then silu(gate) * up
-// (src/model.rs:490-501).  One wave per output row, the whole row in one pass
-// (cols <= 64 * UNR float4s): every load -- both weight rows, x, the partial
-// vectors, the norm weight -- is issued before the first use, so the kernel
-// waits for memory once.  The wave of row 0 writes the summed row to xout (the
-// residual the down product adds to).
-template <int UNR, int NP, int R>
-__global__ __launch_bounds__(256) void gemv_swiglu_parts_kernel(const GemvArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
-    if (row0 >= a.rows) return;  // whole waves only; no barriers below
+// One token, rows of up to 64 * UNR float4s (one pass): the input row is
+// staged through LDS once per workgroup instead of being read by every wave.
+// Thread t owns float4s t, t + 256, ... of the row: it loads x (plus, with
+// NP > 0, the a.nparts partial vectors added in order -- the fused decode's
+// per-unit output projections, the residual add of src/model.rs:486-487 --
+// and the block-0 threads write that sum to a.xout), the norm weight, and its
+// share of the sum of squares; the 4 waves' sums meet in LDS in a fixed order.
+// Each wave owns R output rows, whose weights it requests first, so the
+// kernel waits for memory once; epilogues as gemv_kernel's.
+template <int R, int UNR, int EPI, bool NORM, int NP>
+__global__ __launch_bounds__(256) void gemv1_kernel(const GemvArgs a) {
+    static_assert(EPI != kEpiSwiglu || R == 1, "SwiGLU pairs one gate row with one up row");
+    constexpr int XK = (64 * UNR + 255) / 256;  // float4s of the row per thread
+    __shared__ f4 sx[256 * XK];
+    __shared__ f4 sg[NORM ? 256 * XK : 1];
+    __shared__ float sss[4];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, t = threadIdx.x;
+    const int row0 = (blockIdx.x * 4 + w) * R;
+    const bool live = row0 < a.rows;  // every wave reaches the barrier
     const int C4 = a.cols >> 2;
     const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    const f4 *X = reinterpret_cast<const f4 *>(a.x);
-    const f4 *G = reinterpret_cast<const f4 *>(a.norm);
-    f4 wg[R][UNR], wu[R][UNR], xv[UNR], gv[UNR], pv[NP][UNR];
+
+    // Loads from clamped, in-bounds indices with no condition, and selects
+    // afterwards: a load under a per-lane condition becomes an exec-mask
+    // branch of its own, which serialises the issue of the loads.
+    f4 wv[R][UNR], wv2[UNR];
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const int row = min(row0 + r, a.rows - 1);
-        const f4 *Wg = reinterpret_cast<const f4 *>(a.w + (size_t)row * a.cols);
-        const f4 *Wu = reinterpret_cast<const f4 *>(a.w2 + (size_t)row * a.cols);
+        const f4 *W = reinterpret_cast<const f4 *>(a.w + (size_t)min(row0 + r, a.rows - 1) * a.cols);
 #pragma unroll
-        for (int u = 0; u < UNR; u++) {
-            const int c = lane + 64 * u;
-            wg[r][u] = c < C4 ? __builtin_nontemporal_load(Wg + c) : zero;
-            wu[r][u] = c < C4 ? __builtin_nontemporal_load(Wu + c) : zero;
-        }
+        for (int u = 0; u < UNR; u++) wv[r][u] = __builtin_nontemporal_load(W + min(lane + 64 * u, C4 - 1));
+    }
+    if constexpr (EPI == kEpiSwiglu) {
+        const f4 *W2 = reinterpret_cast<const f4 *>(a.w2 + (size_t)min(row0, a.rows - 1) * a.cols);
+#pragma unroll
+        for (int u = 0; u < UNR; u++) wv2[u] = __builtin_nontemporal_load(W2 + min(lane + 64 * u, C4 - 1));
+    }
+    float resid[EPI == kEpiResid ? R : 1];
+    if constexpr (EPI == kEpiResid) {
+        const float *src = a.resid ? a.resid : a.out0;
+#pragma unroll
+        for (int r = 0; r < R; r++) resid[r] = src[min(row0 + r, a.rows - 1)];
+    }
+    f4 xv[XK], gv[XK], pv[NP > 0 ? NP : 1][XK];
+#pragma unroll
+    for (int k = 0; k < XK; k++) {
+        const int c = min(t + 256 * k, C4 - 1);
+        xv[k] = reinterpret_cast<const f4 *>(a.x)[c];
+        if (NORM) gv[k] = reinterpret_cast<const f4 *>(a.norm)[c];
+#pragma unroll
+        for (int p = 0; p < NP; p++)
+            pv[p][k] = reinterpret_cast<const f4 *>(a.parts + (size_t)min(p, a.nparts - 1) * a.cols)[c];
     }
 #pragma unroll
     for (int u = 0; u < UNR; u++) {
-        const int c = lane + 64 * u;
-        xv[u] = c < C4 ? X[c] : zero;
-        gv[u] = c < C4 ? G[c] : zero;
+        const bool in = lane + 64 * u < C4;
 #pragma unroll
-        for (int p = 0; p < NP; p++)
-            pv[p][u] = (p < a.nparts && c < C4) ? reinterpret_cast<const f4 *>(a.parts + (size_t)p * a.cols)[c] : zero;
+        for (int r = 0; r < R; r++) wv[r][u] = in ? wv[r][u] : zero;
+        if (EPI == kEpiSwiglu) wv2[u] = in ? wv2[u] : zero;
     }
     float ss = 0.0f;
 #pragma unroll
-    for (int u = 0; u < UNR; u++) {
+    for (int k = 0; k < XK; k++) {
+        const bool in = t + 256 * k < C4;
+        xv[k] = in ? xv[k] : zero;
+        if (NORM) gv[k] = in ? gv[k] : zero;
 #pragma unroll
         for (int p = 0; p < NP; p++)
-            if (p < a.nparts) xv[u] += pv[p][u];
-        ss = dot4(xv[u], xv[u], ss);
-    }
-    if (row0 == 0) {
-#pragma unroll
-        for (int u = 0; u < UNR; u++) {
-            const int c = lane + 64 * u;
-            if (c < C4) reinterpret_cast<f4 *>(a.xout)[c] = xv[u];
+            if (p < a.nparts) xv[k] += in ? pv[p][k] : zero;
+        const int c = t + 256 * k;
+        sx[c] = xv[k];
+        if (NORM) {
+            sg[c] = gv[k];
+            ss = dot4(xv[k], xv[k], ss);
         }
+        if (NP > 0 && blockIdx.x == 0 && c < C4) reinterpret_cast<f4 *>(a.xout)[c] = xv[k];
     }
-    ss = wave_sum(ss);
-    const float scale = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
-    float acc[R], acc2[R];
+    if (NORM) {
+        ss = wave_sum(ss);
+        if (lane == 0) sss[w] = ss;
+    }
+    __syncthreads();
+    float scale = 1.0f;
+    if (NORM) {
+        // rmsnorm (src/kernels.rs:343-349): xn = x * scale * g
+        ss = (sss[0] + sss[1]) + (sss[2] + sss[3]);
+        scale = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+    }
+    if (!live) return;
+    float acc[R], acc2 = 0.0f;
 #pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = acc2[r] = 0.0f;
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
 #pragma unroll
     for (int u = 0; u < UNR; u++) {
-        const f4 x = xv[u] * scale * gv[u];
+        const int c = lane + 64 * u;
+        if (c >= C4) break;
+        f4 x = sx[c];
+        if (NORM) x = x * scale * sg[c];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            acc[r] = dot4(wg[r][u], x, acc[r]);
-            acc2[r] = dot4(wu[r][u], x, acc2[r]);
-        }
+        for (int r = 0; r < R; r++) acc[r] = dot4(wv[r][u], x, acc[r]);
+        if (EPI == kEpiSwiglu) acc2 = dot4(wv2[u], x, acc2);
     }
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        acc[r] = wave_sum(acc[r]);
-        acc2[r] = wave_sum(acc2[r]);
-        if (lane == 0 && row0 + r < a.rows) a.out0[row0 + r] = acc[r] / (1.0f + expf(-acc[r])) * acc2[r];
+    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+    if (EPI == kEpiSwiglu) acc2 = wave_sum(acc2);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int row = row0 + r;
+            if (row >= a.rows) break;
+            const float d = acc[r];
+            if (EPI == kEpiStore || EPI == kEpiArgmax) {
+                a.out0[row] = d;
+            } else if (EPI == kEpiResid) {
+                a.out0[row] = resid[r] + d;
+            } else if (EPI == kEpiQkv) {
+                if (row < a.split0)
+                    a.out0[row] = d;
+                else if (row < a.split1)
+                    a.out1[row - a.split0] = d;
+                else
+                    a.out2[row - a.split1] = d;
+            } else {  // silu_mul: g / (1 + exp(-g)) * u
+                a.out0[row] = d / (1.0f + expf(-d)) * acc2;
+            }
+        }
+        if constexpr (EPI == kEpiArgmax) {
+            // the wave's rows in increasing order; argmax_kernel reduces the pairs
+            static_assert(R == kArgmaxRows, "one pair per kArgmaxRows rows");
+            float bv = -INFINITY;
+            int bi = 0x7fffffff;
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (row0 + r < a.rows) arg_better(acc[r], row0 + r, bv, bi);
+            reinterpret_cast<float2 *>(a.out1)[row0 / R] = make_float2(bv, __int_as_float(bi));
+        }
     }
 }
 
@@ -502,17 +564,51 @@ hipError_t gemv_launch(const GemvArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// One token: 8 float4s per lane per pass (rows up to 2048 floats in one pass);
-// the LM head (kEpiStore) takes 4 rows per wave to keep more of its 100+ MB in
-// flight per wave.  Several tokens: 4 per wave, 4 float4s per lane per pass.
+template <int R, int UNR, int EPI>
+hipError_t gemv1_launch_unr(const GemvArgs &a, hipStream_t s) {
+    const int waves = (a.rows + R - 1) / R;
+    const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+    if (a.parts)
+        hipLaunchKernelGGL((gemv1_kernel<R, UNR, EPI, true, kMaxParts>), grid, block, 0, s, a);
+    else if (a.norm)
+        hipLaunchKernelGGL((gemv1_kernel<R, UNR, EPI, true, 0>), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((gemv1_kernel<R, UNR, EPI, false, 0>), grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
+// The unroll that covers the row (64 lanes x UNR float4s) with the fewest
+// spare slots: every slot is a load (clamped in bounds), so spare ones cost
+// load instructions (576 floats: 3; 1536: 6).
+template <int R, int EPI>
+hipError_t gemv1_launch(const GemvArgs &a, hipStream_t s) {
+    const int need = ((a.cols >> 2) + 63) / 64;
+    if (need <= 2) return gemv1_launch_unr<R, 2, EPI>(a, s);
+    if (need <= 3) return gemv1_launch_unr<R, 3, EPI>(a, s);
+    if (need <= 4) return gemv1_launch_unr<R, 4, EPI>(a, s);
+    if (need <= 6) return gemv1_launch_unr<R, 6, EPI>(a, s);
+    if (need <= 8) return gemv1_launch_unr<R, 8, EPI>(a, s);
+    return hipErrorInvalidValue;
+}
+
+// One token: one row per wave (the LM head, kEpiStore / kEpiArgmax, 4 rows per
+// wave to keep more of its 100+ MB in flight per wave), the input row through
+// LDS when it fits one pass (64 * 8 float4s), else gemv_kernel.  Several
+// tokens: 4 per wave, 4 float4s per lane per pass.
 template <int EPI>
 hipError_t gemv_epi(const GemvArgs &a, hipStream_t s) {
+    const bool one_pass = a.cols <= 4 * 64 * 8;
     if constexpr (EPI == kEpiArgmax) {
         if (a.t != 1 || !a.out1) return hipErrorInvalidValue;
+        if (a.cols <= 4 * 64 * 4) return gemv1_launch<kArgmaxRows, EPI>(a, s);
         return gemv_launch<1, kArgmaxRows, 4, EPI>(a, s);
     } else {
         if (a.t > 1) return gemv_launch<4, 1, 4, EPI>(a, s);
-        if constexpr (EPI == kEpiStore) return gemv_launch<1, 4, 4, EPI>(a, s);
+        if constexpr (EPI == kEpiStore) {
+            if (a.cols <= 4 * 64 * 4) return gemv1_launch<4, EPI>(a, s);
+            return gemv_launch<1, 4, 4, EPI>(a, s);
+        }
+        if (one_pass) return gemv1_launch<1, EPI>(a, s);
         return gemv_launch<1, 1, 8, EPI>(a, s);
     }
 }
@@ -524,13 +620,9 @@ hipError_t launch_gemv(int epi, const GemvArgs &a, hipStream_t s) {
     if (a.parts) {
         // the gate/up product after the fused decode + output projection
         if (epi != kEpiSwiglu || a.t != 1 || !a.norm || !a.xout || a.nparts < 1 || a.nparts > kMaxParts ||
-            a.cols > 4 * 64 * 4)
+            a.cols > 4 * 64 * 8)
             return hipErrorInvalidValue;
-        // one row per wave: more waves in flight beat sharing the input row
-        // (2 rows per wave measured 4% slower end to end, 4 rows 14%)
-        const dim3 grid((unsigned)((a.rows + 3) / 4)), block(256);
-        hipLaunchKernelGGL((gemv_swiglu_parts_kernel<4, kMaxParts, 1>), grid, block, 0, s, a);
-        return hipGetLastError();
+        return gemv1_launch<1, kEpiSwiglu>(a, s);
     }
     switch (epi) {
     case kEpiStore: return gemv_epi<kEpiStore>(a, s);

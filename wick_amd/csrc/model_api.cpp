@@ -218,10 +218,10 @@ int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, 
     hipError_t e = wick::launch_embed(m->embed, tok_dev, m->x, t, c.hidden, s, counters);
     if (e != hipSuccess) return hip_fail(e, "embed kernel launch");
     // the gate/up product takes at most kMaxParts partial vectors of up to
-    // 1024 floats (one pass of its waves)
+    // 2048 floats (its input row in one pass)
     const int group = c.heads / c.kv_heads;
     const bool fusable = t == 1 && c.kv_heads * ((group + wick::kTileRows - 1) / wick::kTileRows) <= wick::kMaxParts &&
-                         c.hidden <= 1024;
+                         c.hidden <= 2048;
     for (int li = 0; li < c.layers; li++) {
         const wick_hip_model::Layer &L = m->layers[li];
         wick::GemvArgs g{};

@@ -35,7 +35,7 @@ struct GemvArgs {
     int split0, split1;   // kEpiQkv: rows [0,split0) -> out0, [split0,split1) -> out1, the rest -> out2
     int rows, cols, t;
     float eps;
-    // kEpiSwiglu, one token, cols <= 1024: the input row is x + parts[0] + ...
+    // kEpiSwiglu, one token, cols <= 2048: the input row is x + parts[0] + ...
     // + parts[nparts-1] (nparts <= kMaxParts partial vectors of cols floats,
     // added in that order: the fused decode's per-unit output projections);
     // the wave of row 0 also writes that sum to xout.  Null parts: x as is.
