@@ -571,6 +571,103 @@ __device__ __forceinline__ void lean_step(const LeanGroup<D, TG> &t, const f4 (&
     if constexpr (LAZY) __builtin_amdgcn_s_setprio(0);
 }
 
+// ------------------------------------------------------------------ VALU decode core
+//
+// For a decode unit of NC <= 4 query heads (GQA groups of at most 4) the
+// 16-column MFMA tiles leave at least 12 of their 16 columns idle, and
+// gfx950's VALU FMAs run at the same f32 rate as its MFMAs, so this core runs
+// the products on the VALU (head_dim 64).  A wave steps over groups of 32
+// keys:
+//   QK: lane (key kl = l/2, half hh = l%2) holds float4s 2j + hh (j < 8) of
+//       its key's K row and of each head's q row: 8 dot4s per head, then the
+//       pair's halves are added (DPP xor 1).  Scores are scaled into log2
+//       units after the dot (q is not pre-scaled here).
+//   softmax: per head, the wave's max (DPP / permlane), exp2, the sum over
+//       the 32 keys; the weights go through the wave's own LDS slice.
+//   PV: lane (dims 4*(l%16).., key group kq = l/16) accumulates keys kq + 4k
+//       (k < 8) -- each V load instruction reads 4 whole rows, 1 KiB -- and the
+//       4 key groups are summed across rows (permlane16/32 swaps) at the end.
+// The wave's (m, l, O) per head leave through sm_m / sm_l / sm_o in the layout
+// the workgroup merge reads.
+template <int NC, int NW>
+__device__ __forceinline__ void valu_core(const float *__restrict__ Kh, const float *__restrict__ Vh,
+                                          const f4 (&qr)[NC][8], float qf, int kbeg, int kend, int w, int lane,
+                                          float (&swts)[NW][32][4], float (&sm_m)[NW][16], float (&sm_l)[NW][16],
+                                          float (&sm_o)[NW][16][64]) {
+    constexpr int D = 64, GK = 32;
+    const int hh = lane & 1, kl = lane >> 1;
+    const int dq = lane & 15, kq = lane >> 4;
+    float m[NC], l[NC];
+    f4 o[NC];
+#pragma unroll
+    for (int h = 0; h < NC; h++) {
+        m[h] = -INFINITY;
+        l[h] = 0.f;
+        o[h] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int p0 = kbeg + GK * w; p0 < kend; p0 += NW * GK) {
+        const int last = kend - 1;
+        // the group's K and V rows, clamped to the chunk (masked below)
+        const float *kr = Kh + (size_t)min(p0 + kl, last) * D + 4 * hh;
+        f4 kv[8], vv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) kv[j] = *reinterpret_cast<const f4 *>(kr + 8 * j);
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            vv[k] = *reinterpret_cast<const f4 *>(Vh + (size_t)min(p0 + kq + 4 * k, last) * D + 4 * dq);
+        const bool valid = p0 + kl < kend;
+        float s[NC];
+#pragma unroll
+        for (int h = 0; h < NC; h++) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                acc = fmaf(kv[j].x, qr[h][j].x, acc);
+                acc = fmaf(kv[j].y, qr[h][j].y, acc);
+                acc = fmaf(kv[j].z, qr[h][j].z, acc);
+                acc = fmaf(kv[j].w, qr[h][j].w, acc);
+            }
+            acc += dpp_f<kDppQuadXor1>(acc);  // both lanes of the key: the whole dot
+            s[h] = valid ? acc * qf : -INFINITY;
+        }
+#pragma unroll
+        for (int h = 0; h < NC; h++) {
+            const float mnew = fmaxf(m[h], wave_max(s[h]));  // key p0 is valid: finite
+            const float alpha = exp2_fast(m[h] - mnew);      // 0 from the initial -inf
+            const float e = exp2_fast(s[h] - mnew);
+            l[h] = l[h] * alpha + wave_sum(hh == 0 ? e : 0.f);
+            o[h] *= alpha;
+            m[h] = mnew;
+            if (hh == 0) swts[w][kl][h] = e;
+        }
+        // the wave reads back its own LDS writes (in order within a wave)
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const f4 wk = *reinterpret_cast<const f4 *>(&swts[w][kq + 4 * k][0]);
+#pragma unroll
+            for (int h = 0; h < NC; h++) o[h] += wk[h] * vv[k];
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < NC; h++) {
+        o[h].x = rows_sum(o[h].x);
+        o[h].y = rows_sum(o[h].y);
+        o[h].z = rows_sum(o[h].z);
+        o[h].w = rows_sum(o[h].w);
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int h = 0; h < NC; h++) *reinterpret_cast<f4 *>(&sm_o[w][h][4 * dq]) = o[h];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int h = 0; h < NC; h++) {
+            sm_m[w][h] = m[h];
+            sm_l[w][h] = l[h];
+        }
+    }
+}
+
 // ------------------------------------------------------------------ decode
 
 // Partial states of the split-K decode, per (unit, column): O [units][16][256][D],
@@ -616,13 +713,17 @@ struct DecodeSpace {
 // computes the unit's attention (every row block of a unit repeats it; each
 // writes the same prepared k/v bits), keeps the normalised output in LDS and
 // writes the unit's partial product for its rows.
-template <int D, bool PREP, bool PP = (D < 128), int NW = 4, int TG = Shape<D>::TG, bool OPROJ = false>
+// NC > 0 (head_dim 64, exactly NC <= 4 query heads per unit): the products
+// run on the VALU core (valu_core) instead of the MFMA tiles.
+template <int D, bool PREP, bool PP = (D < 128), int NW = 4, int TG = Shape<D>::TG, bool OPROJ = false, int NC = 0>
 __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
     using S = Shape<D>;
+    static_assert(NC == 0 || (D == 64 && NC <= 4), "the VALU core is for head_dim 64 and at most 4 heads");
     __shared__ float sm_m[NW][16], sm_l[NW][16];
     __shared__ __attribute__((aligned(16))) float sm_o[NW][16][D];
     __shared__ float sq[PREP ? 16 : 1][D];  // prepared q rows (PREP)
     __shared__ float satt[OPROJ ? 16 * D : 1];  // normalised output of the unit's heads (OPROJ)
+    __shared__ __attribute__((aligned(16))) float swts[NC > 0 ? NW : 1][32][4];  // VALU core weights
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int units = a.kv_heads * a.hslices;
@@ -682,10 +783,26 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
                               nullptr, nullptr, lane & 15, lane & 48);
         }
         __syncthreads();
-        qkeep = load_q_raw<D>(sq[col], sq[0], col < ncols, lane, q);
-    } else {
+        if constexpr (NC == 0) qkeep = load_q_raw<D>(sq[col], sq[0], col < ncols, lane, q);
+    } else if constexpr (NC == 0) {
         qkeep = load_q_raw<D>(a.q + (size_t)(head0 + col) * D, a.q + (size_t)head0 * D, col < ncols, lane, q);
     }
+
+    if constexpr (NC > 0) {
+        // the unit's NC q rows, the lane's float4s 2j + hh of each
+        f4 qr[NC > 0 ? NC : 1][8];
+        const int hh = lane & 1;
+#pragma unroll
+        for (int h = 0; h < NC; h++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                if constexpr (PREP)
+                    qr[h][j] = *reinterpret_cast<const f4 *>(&sq[h][8 * j + 4 * hh]);
+                else
+                    qr[h][j] = *reinterpret_cast<const f4 *>(a.q + (size_t)(head0 + h) * D + 8 * j + 4 * hh);
+            }
+        valu_core<NC, NW>(Kh, Vh, qr, a.scale * kLog2e, kbeg, kend, w, lane, swts, sm_m, sm_l, sm_o);
+    } else {
 
     WaveState<D> st;
     if constexpr (D >= 64) {
@@ -759,6 +876,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
     for (int db = 0; db < S::DB; db++)
 #pragma unroll
         for (int r = 0; r < 4; r++) sm_o[w][col][out_dim<D>(g, r, db)] = st.o[db][r];
+    }  // MFMA core
     __syncthreads();
 
     // Merge the NW waves of this workgroup (maxima in log2 units).  Wave 0
@@ -1299,6 +1417,25 @@ int decode_blocks_per_cu(int head_dim) {
     return (e == hipSuccess && n > 0) ? n : 1;
 }
 
+// decode_kernel<D, ...> launched with the VALU core when the unit holds at
+// most 4 query heads at head_dim 64 (the template's NC = the group).
+template <int D, bool PREP, bool PP, int NW, bool OPROJ = false>
+void launch_decode_core(const DecodeArgs &a, dim3 grid, hipStream_t s) {
+    constexpr int TG = Shape<D>::TG;
+    const dim3 block(64 * NW);
+    const int nc = (D == 64 && a.group <= 4) ? a.group : 0;
+    if constexpr (D == 64) {
+        switch (nc) {
+        case 1: hipLaunchKernelGGL((decode_kernel<D, PREP, false, NW, TG, OPROJ, 1>), grid, block, 0, s, a); return;
+        case 2: hipLaunchKernelGGL((decode_kernel<D, PREP, false, NW, TG, OPROJ, 2>), grid, block, 0, s, a); return;
+        case 3: hipLaunchKernelGGL((decode_kernel<D, PREP, false, NW, TG, OPROJ, 3>), grid, block, 0, s, a); return;
+        case 4: hipLaunchKernelGGL((decode_kernel<D, PREP, false, NW, TG, OPROJ, 4>), grid, block, 0, s, a); return;
+        default: break;
+        }
+    }
+    hipLaunchKernelGGL((decode_kernel<D, PREP, PP, NW, TG, OPROJ, 0>), grid, block, 0, s, a);
+}
+
 template <int D>
 void launch_decode_d(const DecodeArgs &a, int grid, hipStream_t s) {
     if constexpr (D <= 64) {
@@ -1306,13 +1443,13 @@ void launch_decode_d(const DecodeArgs &a, int grid, hipStream_t s) {
             // one chunk per unit: 8 waves, each with at most one or two groups
             const bool one8 = a.chunk <= 8 * Shape<D>::TG * 16;
             if (a.prep && one8)
-                hipLaunchKernelGGL((decode_kernel<D, true, false, 8>), dim3(grid), dim3(512), 0, s, a);
+                launch_decode_core<D, true, false, 8>(a, dim3(grid), s);
             else if (a.prep)
-                hipLaunchKernelGGL((decode_kernel<D, true, true, 8>), dim3(grid), dim3(512), 0, s, a);
+                launch_decode_core<D, true, true, 8>(a, dim3(grid), s);
             else if (one8)
-                hipLaunchKernelGGL((decode_kernel<D, false, false, 8>), dim3(grid), dim3(512), 0, s, a);
+                launch_decode_core<D, false, false, 8>(a, dim3(grid), s);
             else
-                hipLaunchKernelGGL((decode_kernel<D, false, true, 8>), dim3(grid), dim3(512), 0, s, a);
+                launch_decode_core<D, false, true, 8>(a, dim3(grid), s);
             return;
         }
     }
@@ -1321,16 +1458,16 @@ void launch_decode_d(const DecodeArgs &a, int grid, hipStream_t s) {
     if constexpr (D < 128) {
         if (one_group) {
             if (a.prep)
-                hipLaunchKernelGGL((decode_kernel<D, true, false>), dim3(grid), dim3(256), 0, s, a);
+                launch_decode_core<D, true, false, 4>(a, dim3(grid), s);
             else
-                hipLaunchKernelGGL((decode_kernel<D, false, false>), dim3(grid), dim3(256), 0, s, a);
+                launch_decode_core<D, false, false, 4>(a, dim3(grid), s);
             return;
         }
     }
     if (a.prep)
-        hipLaunchKernelGGL((decode_kernel<D, true>), dim3(grid), dim3(256), 0, s, a);
+        launch_decode_core<D, true, (D < 128), 4>(a, dim3(grid), s);
     else
-        hipLaunchKernelGGL((decode_kernel<D, false>), dim3(grid), dim3(256), 0, s, a);
+        launch_decode_core<D, false, (D < 128), 4>(a, dim3(grid), s);
 }
 
 hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_t s) {
@@ -1362,9 +1499,9 @@ hipError_t launch_decode_oproj(int head_dim, DecodeArgs a, hipStream_t s) {
     const int blocks = (a.hidden + 8 * kOprojRows - 1) / (8 * kOprojRows);
     const dim3 grid((unsigned)(a.kv_heads * a.hslices * blocks));
     if (head_dim == 64)
-        hipLaunchKernelGGL((decode_kernel<64, true, false, 8, 2, true>), grid, dim3(512), 0, s, a);
+        launch_decode_core<64, true, false, 8, true>(a, grid, s);
     else
-        hipLaunchKernelGGL((decode_kernel<128, true, false, 8, 1, true>), grid, dim3(512), 0, s, a);
+        launch_decode_core<128, true, false, 8, true>(a, grid, s);
     return hipGetLastError();
 }
 

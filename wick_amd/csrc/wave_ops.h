@@ -39,4 +39,24 @@ __device__ __forceinline__ float wave_sum(float v) {
     return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
+// Maximum over the 64 lanes (fmaxf at every step); every lane gets the same bits.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppRowMirror>(v));
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
+// Sum of the 4 lanes l, l^16, l^32, l^48 (the same column of every row of 16).
+__device__ __forceinline__ float rows_sum(float v) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
 }  // namespace wick
