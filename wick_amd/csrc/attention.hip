@@ -1496,12 +1496,16 @@ hipError_t launch_decode_oproj(int head_dim, DecodeArgs a, hipStream_t s) {
     // waves x 32 keys at head_dim 64; head_dim 128 loops over 16-key groups)
     if (!a.prep || !decode_oproj_supported(head_dim, a.group, a.nchunks) || a.chunk > 8 * 2 * 16)
         return hipErrorInvalidValue;
-    const int blocks = (a.hidden + 8 * kOprojRows - 1) / (8 * kOprojRows);
+    // 8 waves split the keys, one wo row each: the widest grid measured best
+    // (1, 2, 4 rows per wave: 216 / 108 / 54 workgroups for SmolLM2, e2e
+    // 1845 / 1824 / 1795 tok/s; 4 waves per workgroup 1728)
+    constexpr int NW = 8;
+    const int blocks = (a.hidden + NW * kOprojRows - 1) / (NW * kOprojRows);
     const dim3 grid((unsigned)(a.kv_heads * a.hslices * blocks));
     if (head_dim == 64)
-        launch_decode_core<64, true, false, 8, true>(a, grid, s);
+        launch_decode_core<64, true, false, NW, true>(a, grid, s);
     else
-        launch_decode_core<128, true, false, 8, true>(a, grid, s);
+        launch_decode_core<128, true, false, NW, true>(a, grid, s);
     return hipGetLastError();
 }
 

@@ -49,7 +49,7 @@ struct DecodeArgs {
 
 // Fused output projection: rows per wave, and the most 64-column chunks of a
 // unit's output (ncols * head_dim <= 64 * kOprojChunks).
-constexpr int kOprojRows = 4;
+constexpr int kOprojRows = 1;
 constexpr int kOprojChunks = 4;
 
 struct PrefillArgs {
