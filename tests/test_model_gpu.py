@@ -234,6 +234,40 @@ def test_decode_replay_matches_step_by_step(name):
     assert chain == steps
 
 
+@pytest.mark.parametrize("shape", ["d64-g1-kv4", "d64-g2-kv3", "d64-g4-kv2", "d128-g2-kv2", "d64-g3-kv4-bias-qknorm"])
+def test_fused_projection_and_valu_core_shapes(shape):
+    """One-token forwards take the fused attention + output projection (partial
+    products per unit, summed by the gate/up prologue) and, at head_dim 64 with
+    groups of at most 4, the VALU attention core.  Shapes around their limits:
+    groups 1, 2, 3, 4, up to 4 kv heads (the most partial vectors), head_dim
+    128, biases and QK-norm.  20-token prompt, then 30 greedy steps across the
+    32- and 64-key tile boundaries: logits within 1e-4 of the CPU oracle and
+    the same ids at every step."""
+    d, g, kvh = {"d64-g1-kv4": (64, 1, 4), "d64-g2-kv3": (64, 2, 3), "d64-g4-kv2": (64, 4, 2),
+                 "d128-g2-kv2": (128, 2, 2), "d64-g3-kv4-bias-qknorm": (64, 3, 4)}[shape]
+    heads = g * kvh
+    extra = shape.endswith("bias-qknorm")
+    cfg = Config("qwen3" if extra else "llama", 192, 256, 2, heads, kvh, d, 300, rms_eps=1e-5, rope_theta=10000.0,
+                 attn_bias=extra, qk_norm=extra)
+    w = random_weights(cfg, seed=31, std=0.08)
+    if extra:
+        w = _bias_and_norms(cfg, w, 32)
+    prompt = [int(x) for x in random_prompt(33, 20, cfg.vocab)]
+    om = ol.OracleModel(cfg, w)
+    ost = om.new_state(64)
+    want = om.forward(ost, prompt)
+    with DeviceModel(cfg, w) as m:
+        cache = m.new_cache(64)
+        got = m.forward(cache, prompt)
+        for step in range(30):
+            diff = np.abs(got[0] - want[0]).max()
+            assert diff < 1e-4, f"{shape}: step {step} logits differ by {diff}"
+            tok = ol.argmax(want[0])
+            assert int(np.argmax(got[0])) == tok, f"{shape}: step {step}"
+            got = m.forward(cache, [tok])
+            want = om.forward(ost, [tok])
+
+
 def test_prefill_chunks_of_256():
     """A 300-token prompt runs as chunks of 256 + 44 (src/engine.rs:107, :134)."""
     cfg, w, exp = fixture("qwen3-qknorm-f32")
