@@ -346,45 +346,69 @@ def measure_long_decode(torch, kv_cls, native, dev, steps):
 
 def measure_long_decode_steps(torch, kv, g, inv, dev, nsteps=64):
     """configs[4] as a decode loop (Session::step -> Model::forward, /root/reference/src/engine.rs:142-145,
-    src/model.rs:481-485): the cache holds 65536 - 64 positions; each of 64 steps appends the new
-    token's k and v rows (RoPE applied) at the next position of every layer and attends over the
-    grown cache, so the launch plan follows the length.  Timed with HIP events over all 64 x 32
-    (append, attention) pairs, eager launches on the bench stream."""
+    src/model.rs:464-485): the cache holds 65536 - 64 positions; each of 64 steps hands every layer the
+    token's raw q, k and v projections, whose k is RoPE'd and appended with v at the next position
+    before attention over the grown cache, so the launch plan follows the length.  Timed with HIP
+    events over all 64 x 32 per-layer calls, eager launches on the bench stream, in two forms:
+    wick_hip_attend_device (preparation and append in the decode kernel's prologue: the model's
+    per-layer call) and a separate append followed by attention on the prepared rows."""
     c = LONG
     kvd, hd = c["kv_heads"] * c["d"], c["heads"] * c["d"]
     base = c["L"] - nsteps
+    kv.set_rope(inv.cpu().numpy())
+    for layer in range(c["layers"]):
+        kv.set_prep(layer, c["heads"], eps=1e-5)
     pos = torch.arange(base, c["L"], device=dev)
-    krows = rope_torch(torch.randn(nsteps, kvd, generator=g, device=dev), c["kv_heads"], c["d"], pos, inv).contiguous()
+    kraw = torch.randn(nsteps, kvd, generator=g, device=dev)
     vrows = torch.randn(nsteps, kvd, generator=g, device=dev)
-    q = torch.randn(nsteps, c["layers"], hd, generator=g, device=dev)
-    q = rope_torch(q.view(nsteps * c["layers"], hd), c["heads"], c["d"], pos.repeat_interleave(c["layers"]),
-                   inv).view(nsteps, c["layers"], hd).contiguous()
+    qraw = torch.randn(nsteps, c["layers"], hd, generator=g, device=dev)
+    krows = rope_torch(kraw.clone(), c["kv_heads"], c["d"], pos, inv).contiguous()
+    q = rope_torch(qraw.clone().view(nsteps * c["layers"], hd), c["heads"], c["d"],
+                   pos.repeat_interleave(c["layers"]), inv).view(nsteps, c["layers"], hd).contiguous()
     att = torch.empty(c["layers"], hd, device=dev)
 
-    def run():
+    def run_attend():
+        for s in range(nsteps):
+            kp, vp = kraw[s].data_ptr(), vrows[s].data_ptr()
+            for layer in range(c["layers"]):
+                kv.attend_device(layer, c["heads"], qraw[s, layer].data_ptr(), kp, vp, 1, base + s,
+                                 att[layer].data_ptr())
+
+    def run_append():
         for s in range(nsteps):
             kp, vp = krows[s].data_ptr(), vrows[s].data_ptr()
             for layer in range(c["layers"]):
                 kv.append_device(layer, base + s, 1, kp, vp)
                 kv.attention_device(layer, c["heads"], q[s, layer].data_ptr(), 1, base + s,
                                     att[layer].data_ptr())
-    run()  # warm-up: appending the same rows again rewrites the same bits
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    run()
-    e1.record()
-    e1.synchronize()
-    ms = e0.elapsed_time(e1)
+
     pairs = nsteps * c["layers"]
     attn_bytes = sum(decode_bytes(base + s + 1, c["heads"], c["kv_heads"], c["d"]) for s in range(nsteps)) * c["layers"]
     append_bytes = pairs * 2 * 2 * kvd * 4  # k and v rows read and written
-    gbs = (attn_bytes + append_bytes) / (ms * 1e-3) / 1e9
-    return {"what": f"cache at {base} positions, then {nsteps} steps x {c['layers']} layers of (append one k/v row, "
-                    f"attention over {base + 1}..{c['L']} positions); eager launches",
-            "us_per_layer": round(ms * 1e3 / pairs, 2), "ms_per_step": round(ms / nsteps, 3),
-            "bytes": attn_bytes + append_bytes, "GBps": round(gbs, 1),
-            "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "workgroups_last_step": kv.last_grid()}
+
+    def timed(run):
+        run()  # warm-up: a step appends the same rows again, rewriting the same bits
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run()
+        e1.record()
+        e1.synchronize()
+        ms = e0.elapsed_time(e1)
+        gbs = (attn_bytes + append_bytes) / (ms * 1e-3) / 1e9
+        return {"us_per_layer": round(ms * 1e3 / pairs, 2), "ms_per_step": round(ms / nsteps, 3),
+                "GBps": round(gbs, 1), "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+                "workgroups_last_step": kv.last_grid()}
+
+    sep = timed(run_append)
+    out = timed(run_attend)
+    out.update({"what": f"cache at {base} positions, then {nsteps} steps x {c['layers']} layers of wick_hip_attend_device "
+                        f"(raw q/k/v in; k RoPE'd and appended with v at the next position in the decode kernel's "
+                        f"prologue; attention over {base + 1}..{c['L']} positions); eager launches",
+                "bytes": attn_bytes + append_bytes,
+                "append_then_attention": dict(sep, what="the same steps as wick_hip_kv_append_device of the prepared "
+                                                        "rows, then wick_hip_attention_device")})
+    return out
 
 
 def measure_e2e():

@@ -123,8 +123,10 @@ int wick_hip_kv_set_prep(wick_hip_kv *kv, int layer, int heads, const float *bq,
 int wick_hip_attend(wick_hip_kv *kv, int layer, int heads, const float *q, const float *k, const float *v, int t,
                     int start, float *att);
 
-/* As wick_hip_attend on device arrays (16-byte aligned); q_dev is rewritten
- * in place with the prepared q.  Asynchronous on the handle's stream. */
+/* As wick_hip_attend on device arrays (16-byte aligned).  For t > 1, q_dev is
+ * rewritten in place with the prepared q; a single token (t = 1) is prepared
+ * inside the decode kernel and q_dev is left as it is.  Asynchronous on the
+ * handle's stream. */
 int wick_hip_attend_device(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev,
                            const float *v_dev, int t, int start, float *att_dev);
 

@@ -126,6 +126,53 @@ def test_high_positions_use_their_table_rows():
     assert np.array_equal(gv.view(np.uint32), pv.view(np.uint32))
 
 
+def test_long_decode_steps_attend_llama3_8b_shape():
+    """configs[4] as the model's decode loop (Session::step -> Model::forward,
+    /root/reference/src/engine.rs:142-145, src/model.rs:464-485): the cache
+    holds 65472 positions, then 64 steps hand every layer the token's raw q, k
+    and v; single-token attend prepares q in the decode kernel's prologue and
+    appends the RoPE'd k and v at the next position there.  The appended rows
+    are bit-exact against the oracle's preparation, the first and the last
+    step's outputs (65473 and 65536 positions) match the oracle.  Two layers of
+    the config's per-layer shape (Hq 32 / Hkv 8, d 128) keep the host copy
+    small."""
+    heads, kvh, d, L, nsteps, layers = 32, 8, 128, 65536, 64, 2
+    base = L - nsteps
+    inv = ol.rope_inv_freq(500000.0, d)
+    rng = np.random.default_rng(7)
+    ks = [rng.standard_normal((L, kvh * d), dtype=np.float32) for _ in range(layers)]
+    vs = [rng.standard_normal((L, kvh * d), dtype=np.float32) for _ in range(layers)]
+    raw = [[raw_inputs(1000 * layer + s, 1, heads, kvh, d)[:3] for s in range(nsteps)] for layer in range(layers)]
+    outs = {}
+    with DeviceKvCache(layers, L, kvh, d) as kv:
+        kv.set_rope(inv)
+        for layer in range(layers):
+            kv.set_prep(layer, heads, eps=1e-5)
+            kv.append(layer, 0, ks[layer][:base], vs[layer][:base])
+        for s in range(nsteps):
+            for layer in range(layers):
+                q, k, v = raw[layer][s]
+                att = kv.attend(layer, heads, q, k, v, base + s)
+                if s in (0, nsteps - 1):
+                    outs[(layer, s)] = att
+        got = [kv.read(layer, base, nsteps) for layer in range(layers)]
+    pq = {}
+    for layer in range(layers):
+        for s in range(nsteps):
+            q, k, v = raw[layer][s]
+            pq[(layer, s)], pk, pv = ol.prep(q, k, v, heads, kvh, d, base + s, inv, eps=1e-5)
+            ks[layer][base + s], vs[layer][base + s] = pk[0], pv[0]
+        gk, gv = got[layer]
+        assert np.array_equal(gk.view(np.uint32), ks[layer][base:].view(np.uint32)), f"layer {layer}: K rows"
+        assert np.array_equal(gv.view(np.uint32), vs[layer][base:].view(np.uint32)), f"layer {layer}: V rows"
+    for (layer, s), att in outs.items():
+        n = base + s + 1
+        want = ol.attention(pq[(layer, s)], ks[layer][:n], vs[layer][:n], 1, base + s, heads, kvh, d)
+        ok, mabs, mrel = within_tol(att, want)
+        print(f"layer {layer} step {s} ({n} positions): max abs {mabs:.2e} max rel {mrel:.2e}")
+        assert ok, (layer, s, mabs, mrel)
+
+
 def test_attend_device_rewrites_q_in_place():
     torch = pytest.importorskip("torch")
     heads, kv_heads, d, t, start = 16, 8, 128, 64, 0
@@ -148,6 +195,31 @@ def test_attend_device_rewrites_q_in_place():
     assert np.array_equal(gk.view(np.uint32), pk.view(np.uint32))
     assert np.array_equal(gv.view(np.uint32), pv.view(np.uint32))
     ok, mabs, mrel = within_tol(gatt, ol.attention(pq, pk, pv, t, start, heads, kv_heads, d))
+    assert ok, f"max abs {mabs:.3e}, max rel {mrel:.3e}"
+
+
+def test_attend_device_single_token_leaves_q():
+    """t = 1 prepares q inside the decode kernel: q_dev keeps the raw projection."""
+    torch = pytest.importorskip("torch")
+    heads, kv_heads, d = 16, 8, 128
+    inv = ol.rope_inv_freq(1e6, d)
+    q, k, v, b, n = raw_inputs(12, 5, heads, kv_heads, d, bias=True, norm=True)
+    with DeviceKvCache(1, 256, kv_heads, d) as kv:
+        kv.set_rope(inv)
+        register(kv, 0, heads, b, n, 1e-6)
+        kv.attend(0, heads, q[:4], k[:4], v[:4], 0)
+        qd, kd, vd = (torch.from_numpy(np.ascontiguousarray(a[4:])).cuda() for a in (q, k, v))
+        att = torch.empty_like(qd)
+        torch.cuda.synchronize()
+        kv.attend_device(0, heads, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), 1, 4, att.data_ptr())
+        kv.synchronize()
+        gq, gatt = qd.cpu().numpy(), att.cpu().numpy()
+        gk, gv = kv.read(0, 0, 5)
+    assert np.array_equal(gq.view(np.uint32), q[4:].view(np.uint32)), "q_dev changed"
+    pq, pk, pv = ol.prep(q, k, v, heads, kv_heads, d, 0, inv, bias=b, norms=n, eps=1e-6)
+    assert np.array_equal(gk.view(np.uint32), pk.view(np.uint32))
+    assert np.array_equal(gv.view(np.uint32), pv.view(np.uint32))
+    ok, mabs, mrel = within_tol(gatt, ol.attention(pq[4:], pk, pv, 1, 4, heads, kv_heads, d))
     assert ok, f"max abs {mabs:.3e}, max rel {mrel:.3e}"
 
 

@@ -677,17 +677,10 @@ int wick_hip_kv_set_prep(wick_hip_kv *kv, int layer, int heads, const float *bq,
 
 int wick_hip_attend_device(wick_hip_kv *kv, int layer, int heads, float *q_dev, const float *k_dev,
                            const float *v_dev, int t, int start, float *att_dev) {
-    int rc = check_kv(kv, layer);
-    if (rc) return rc;
-    if ((rc = check_span(kv, start, t))) return rc;
-    if (!q_dev || !k_dev || !v_dev || !att_dev) return fail(WICK_HIP_EINVAL, "null q, k, v or att");
-    if ((rc = check_aligned(q_dev, "q_dev")) || (rc = check_aligned(k_dev, "k_dev")) ||
-        (rc = check_aligned(v_dev, "v_dev")) || (rc = check_aligned(att_dev, "att_dev")))
-        return rc;
-    if (heads < 1 || heads % kv->kv_heads != 0)
-        return fail(WICK_HIP_EINVAL, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv->kv_heads);
-    if ((rc = run_prep(kv, layer, heads, q_dev, k_dev, v_dev, t, start))) return rc;
-    return run_attention(kv, layer, heads, q_dev, t, start, att_dev);
+    // one token: preparation and append in the decode kernel's prologue (one
+    // launch, q_dev untouched); a chunk: the preparation kernel (q in place),
+    // then attention
+    return wick::attend_model(kv, layer, heads, q_dev, k_dev, v_dev, t, start, att_dev, nullptr);
 }
 
 int wick_hip_attend(wick_hip_kv *kv, int layer, int heads, const float *q, const float *k, const float *v, int t,
