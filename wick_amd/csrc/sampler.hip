@@ -19,8 +19,9 @@
 //      a stable LSD radix sort of the whole vocabulary in global memory; the
 //      first k entries are the candidates, equal logits ordered by id;
 //   5. softmax at the temperature (:95-98), min-p (:99-104), top-p (:105-115),
-//      the draw (:116-125): f32 operations in wick's order, the running sums
-//      and the draw walked one element at a time by one wave.
+//      the draw (:116-125): f32 operations in wick's order (exp with the bits
+//      of the C library's expf, exp_f32.h), the running sums and the draw
+//      walked one element at a time by one wave.
 // The sums stop early once the next term is at most a quarter ulp of the sum:
 // the terms only shrink (the list is sorted), so no later term can change it.
 #include <hip/hip_runtime.h>
@@ -28,6 +29,7 @@
 #include <climits>
 #include <cmath>
 
+#include "exp_f32.h"
 #include "sampler_kernels.h"
 
 namespace wick {
@@ -84,9 +86,6 @@ __device__ __forceinline__ float key_value(uint32_t key) {
     const uint32_t ord = ~key;
     return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
 }
-
-// f32::exp as exp() in double rounded once to f32.
-__device__ __forceinline__ float exp_f32(float y) { return (float)exp((double)y); }
 
 __device__ __forceinline__ void arg_better(float v, int i, float &bv, int &bi) {
     if (v > bv || (v == bv && i < bi)) {
