@@ -61,22 +61,45 @@ def inv_freq_torch(theta, d, dev):
     return torch.tensor([1.0 / theta ** (2.0 * i / d) for i in range(d // 2)], dtype=torch.float32, device=dev)
 
 
+class Synth:
+    """One benchmark configuration's inputs: N(0, 1) times a scale from wick's generator
+    (xoshiro256** seeded through splitmix64 with the configuration's seed,
+    /root/reference/src/sampler.rs:28-55), made normal by Box-Muller, generated on the
+    device by libwick_probe.so's wick_synth_normal.  The i-th tensor asked for reads
+    substream i of the seed's stream (i long jumps), its rows successive jumps."""
+
+    def __init__(self, torch, dev, seed):
+        import ctypes
+        self.torch, self.dev, self.seed, self.count = torch, dev, seed, 0
+        self.lib = ctypes.CDLL(os.path.join(ROOT, "wick_amd", "libwick_probe.so"))
+        self.lib.wick_synth_normal.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_int,
+                                               ctypes.c_ulonglong, ctypes.c_float, ctypes.c_void_p]
+
+    def normal(self, rows, cols, scale=1.0):
+        x = self.torch.empty(rows, cols, device=self.dev)
+        rc = self.lib.wick_synth_normal(x.data_ptr(), self.count, rows, cols, self.seed, scale,
+                                        self.torch.cuda.current_stream().cuda_stream)
+        if rc:
+            raise RuntimeError(f"wick_synth_normal: HIP error {rc}")
+        self.count += 1
+        return x
+
+
 def setup_decode(torch, kv_cls, dev):
     c = DEC
-    g = torch.Generator(device=dev)
-    g.manual_seed(c["seed"])
+    g = Synth(torch, dev, c["seed"])
     inv = inv_freq_torch(c["theta"], c["d"], dev)
     kv = kv_cls(c["layers"], c["L"], c["kv_heads"], c["d"])
     kv.set_stream(torch.cuda.current_stream().cuda_stream)
     pos = torch.arange(c["L"], device=dev)
     for layer in range(c["layers"]):
-        k = torch.randn(c["L"], c["kv_heads"] * c["d"], generator=g, device=dev)
-        v = torch.randn(c["L"], c["kv_heads"] * c["d"], generator=g, device=dev)
+        k = g.normal(c["L"], c["kv_heads"] * c["d"])
+        v = g.normal(c["L"], c["kv_heads"] * c["d"])
         k = rope_torch(k, c["kv_heads"], c["d"], pos, inv).contiguous()
         kv.append_device(layer, 0, c["L"], k.data_ptr(), v.data_ptr())
         torch.cuda.synchronize()
         del k, v
-    q = torch.randn(c["layers"], c["heads"] * c["d"], generator=g, device=dev)
+    q = g.normal(c["layers"], c["heads"] * c["d"])
     q = rope_torch(q, c["heads"], c["d"], torch.full((c["layers"],), c["L"] - 1, device=dev), inv).contiguous()
     att = torch.empty_like(q)
     return kv, q, att
@@ -198,21 +221,20 @@ def pmc_case_long(torch, kv_cls, dev, layers=4):
     (each 537 MB of K+V, twice the Infinity Cache), one call per layer, then a plain copy
     of known size that calibrates the byte counters."""
     c = LONG
-    g = torch.Generator(device=dev)
-    g.manual_seed(c["seed"])
+    g = Synth(torch, dev, c["seed"])
     inv = inv_freq_torch(c["theta"], c["d"], dev)
     kv = kv_cls(layers, c["L"], c["kv_heads"], c["d"])
     kv.set_stream(torch.cuda.current_stream().cuda_stream)
     pos = torch.arange(c["L"], device=dev)
     for layer in range(layers):
-        k = rope_torch(torch.randn(c["L"], c["kv_heads"] * c["d"], generator=g, device=dev), c["kv_heads"], c["d"],
+        k = rope_torch(g.normal(c["L"], c["kv_heads"] * c["d"]), c["kv_heads"], c["d"],
                        pos, inv).contiguous()
-        v = torch.randn(c["L"], c["kv_heads"] * c["d"], generator=g, device=dev)
+        v = g.normal(c["L"], c["kv_heads"] * c["d"])
         kv.append_device(layer, 0, c["L"], k.data_ptr(), v.data_ptr())
         torch.cuda.synchronize()
         del k, v
     hd = c["heads"] * c["d"]
-    q = rope_torch(torch.randn(layers, hd, generator=g, device=dev), c["heads"], c["d"],
+    q = rope_torch(g.normal(layers, hd), c["heads"], c["d"],
                    torch.full((layers,), c["L"] - 1, device=dev), inv).contiguous()
     att = torch.empty_like(q)
     for layer in range(layers):
@@ -258,8 +280,7 @@ LONG = dict(heads=32, kv_heads=8, d=128, layers=32, L=65536, theta=500000.0, see
 
 def measure_prefill(torch, kv_cls, dev, heads, kv_heads, d, T, start, theta, seed, qk_norm, steps):
     """One layer's attention over T new tokens after `start` cached positions; returns (us, flops)."""
-    g = torch.Generator(device=dev)
-    g.manual_seed(seed)
+    g = Synth(torch, dev, seed)
     inv = inv_freq_torch(theta, d, dev)
     L = start + T
 
@@ -268,11 +289,11 @@ def measure_prefill(torch, kv_cls, dev, heads, kv_heads, d, T, start, theta, see
             return x
         x = x.view(-1, h, d)
         return (x * torch.rsqrt((x * x).mean(-1, keepdim=True) + 1e-6)).view(-1, h * d)
-    q = rope_torch(norm(torch.randn(T, heads * d, generator=g, device=dev), heads), heads, d,
+    q = rope_torch(norm(g.normal(T, heads * d), heads), heads, d,
                    torch.arange(start, L, device=dev), inv).contiguous()
-    k = rope_torch(norm(torch.randn(L, kv_heads * d, generator=g, device=dev), kv_heads), kv_heads, d,
+    k = rope_torch(norm(g.normal(L, kv_heads * d), kv_heads), kv_heads, d,
                    torch.arange(L, device=dev), inv).contiguous()
-    v = torch.randn(L, kv_heads * d, generator=g, device=dev)
+    v = g.normal(L, kv_heads * d)
     att = torch.empty_like(q)
     kv = kv_cls(1, L, kv_heads, d)
     kv.set_stream(torch.cuda.current_stream().cuda_stream)
@@ -288,21 +309,20 @@ def measure_prefill(torch, kv_cls, dev, heads, kv_heads, d, T, start, theta, see
 def measure_long_decode(torch, kv_cls, native, dev, steps):
     """32 layers x 65536 positions (16 GiB of K+V), one token per layer per step."""
     c = LONG
-    g = torch.Generator(device=dev)
-    g.manual_seed(c["seed"])
+    g = Synth(torch, dev, c["seed"])
     inv = inv_freq_torch(c["theta"], c["d"], dev)
     kv = kv_cls(c["layers"], c["L"], c["kv_heads"], c["d"])
     kv.set_stream(torch.cuda.current_stream().cuda_stream)
     pos = torch.arange(c["L"], device=dev)
     for layer in range(c["layers"]):
-        k = rope_torch(torch.randn(c["L"], c["kv_heads"] * c["d"], generator=g, device=dev), c["kv_heads"], c["d"],
+        k = rope_torch(g.normal(c["L"], c["kv_heads"] * c["d"]), c["kv_heads"], c["d"],
                        pos, inv).contiguous()
-        v = torch.randn(c["L"], c["kv_heads"] * c["d"], generator=g, device=dev)
+        v = g.normal(c["L"], c["kv_heads"] * c["d"])
         kv.append_device(layer, 0, c["L"], k.data_ptr(), v.data_ptr())
         torch.cuda.synchronize()
         del k, v
     hd = c["heads"] * c["d"]
-    q = rope_torch(torch.randn(c["layers"], hd, generator=g, device=dev), c["heads"], c["d"],
+    q = rope_torch(g.normal(c["layers"], hd), c["heads"], c["d"],
                    torch.full((c["layers"],), c["L"] - 1, device=dev), inv).contiguous()
     att = torch.empty_like(q)
 
@@ -359,9 +379,9 @@ def measure_long_decode_steps(torch, kv, g, inv, dev, nsteps=64):
     for layer in range(c["layers"]):
         kv.set_prep(layer, c["heads"], eps=1e-5)
     pos = torch.arange(base, c["L"], device=dev)
-    kraw = torch.randn(nsteps, kvd, generator=g, device=dev)
-    vrows = torch.randn(nsteps, kvd, generator=g, device=dev)
-    qraw = torch.randn(nsteps, c["layers"], hd, generator=g, device=dev)
+    kraw = g.normal(nsteps, kvd)
+    vrows = g.normal(nsteps, kvd)
+    qraw = g.normal(nsteps * c["layers"], hd).view(nsteps, c["layers"], hd)
     krows = rope_torch(kraw.clone(), c["kv_heads"], c["d"], pos, inv).contiguous()
     q = rope_torch(qraw.clone().view(nsteps * c["layers"], hd), c["heads"], c["d"],
                    pos.repeat_interleave(c["layers"]), inv).view(nsteps, c["layers"], hd).contiguous()
@@ -417,10 +437,13 @@ def measure_e2e():
     import numpy as np
     from wick_amd.device_model import DeviceModel
     from wick_amd.host import HostModel
-    from wick_amd.synthetic import random_prompt, random_weights, smollm2_135m
+    import torch
+    from wick_amd.synthetic import random_weights, smollm2_135m, wick_prompt
     cfg = smollm2_135m()
-    w = random_weights(cfg, seed=0)
-    prompt = random_prompt(1, 128, cfg.vocab)
+    # weights: wick's generator, seed 0, N(0, 0.02); prompt: seed 1, ids uniform over the vocabulary
+    syn = Synth(torch, "cuda", 0)
+    w = random_weights(cfg, normal=lambda rows, cols, std: syn.normal(rows, cols, std).cpu().numpy())
+    prompt = wick_prompt(1, 128, cfg.vocab)
     n_gen = 64
     # (1) the drop-in: wick's host forward (C++ mirror, projections on the CPU),
     #     with the per-layer preparation, KV cache and attention on the GPU
@@ -641,7 +664,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic",
+        "data": "synthetic: N(0,1) from wick's generator (xoshiro256** seeded by splitmix64, Box-Muller), "
+                "seed 2 for this config (e2e weights 0, prompt 1; prefill 3, chunked 4, long decode 5)",
         "config": {"workload": "decode attention, Qwen2.5-0.5B shape (Hq 14 / Hkv 2, head_dim 64), 24 layers, "
                                "KV cache 32768 positions per layer, f32, one query token per layer",
                    "layers_per_step": c["layers"], "context": c["L"], "decode_workgroups": grid,

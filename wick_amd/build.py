@@ -65,11 +65,14 @@ def build_host():
     return out
 
 
+PROBE_SOURCES = ("roofline_probe.hip", "synth.hip")
+
+
 def build_probe():
-    """Measurement kernels for bench.py (read ceiling, launch floor); not part of
-    the attention path."""
+    """Measurement helpers for bench.py (read ceiling, launch floor, synthetic
+    inputs from wick's generator); not part of the attention path."""
     out = os.path.join(HERE, "libwick_probe.so")
-    _run([HIPCC, *HIP_FLAGS, "-shared", os.path.join(CSRC, "roofline_probe.hip"), "-o", out + ".tmp"])
+    _run([HIPCC, *HIP_FLAGS, "-shared", *(os.path.join(CSRC, f) for f in PROBE_SOURCES), "-o", out + ".tmp"])
     os.replace(out + ".tmp", out)
     return out
 

@@ -3,12 +3,50 @@
 smollm2_135m() is the SmolLM2-135M architecture of the e2e benchmark: Llama, 30 layers,
 hidden 576, 9 query / 3 KV heads, head_dim 64, FFN 1536 SiLU-gated, RMSNorm eps
 1e-5, RoPE theta 10000, vocab 49152, tied embeddings.  Matrices are f32
-N(0, 0.02) drawn with numpy's PCG64 from the given seed, in a fixed order;
-norm weights are 1.0 (the Hugging Face initialisation).
+N(0, std) in a fixed order -- drawn with numpy's PCG64 from the given seed, or by
+a caller-supplied generator (bench.py passes wick's, see `normal` below); norm
+weights are 1.0 (the Hugging Face initialisation).  wick_prompt() draws token
+ids with wick's own generator.
 """
 import numpy as np
 
 from .model import Config
+
+_M64 = (1 << 64) - 1
+
+
+class WickRng:
+    """wick's generator (/root/reference/src/sampler.rs:28-55): xoshiro256** seeded
+    through splitmix64, in Python integers."""
+
+    def __init__(self, seed):
+        z, s = seed & _M64, []
+        for _ in range(4):
+            z = (z + 0x9E3779B97F4A7C15) & _M64
+            x = z
+            x = ((x ^ (x >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+            x = ((x ^ (x >> 27)) * 0x94D049BB133111EB) & _M64
+            s.append(x ^ (x >> 31))
+        self.s = s
+
+    def next_u64(self):
+        s = self.s
+        out = (((s[1] * 5) & _M64) << 7 | ((s[1] * 5) & _M64) >> 57) & _M64
+        out = (out * 9) & _M64
+        t = (s[1] << 17) & _M64
+        s[2] ^= s[0]
+        s[3] ^= s[1]
+        s[1] ^= s[2]
+        s[0] ^= s[3]
+        s[2] ^= t
+        s[3] = ((s[3] << 45) | (s[3] >> 19)) & _M64
+        return out
+
+
+def wick_prompt(seed, n, vocab):
+    """n token ids from wick's generator seeded with `seed`: next_u64() % vocab, in order."""
+    rng = WickRng(seed)
+    return np.array([rng.next_u64() % vocab for _ in range(n)], dtype=np.uint32)
 
 
 def smollm2_135m():
@@ -17,10 +55,15 @@ def smollm2_135m():
                   tie_embeddings=True)
 
 
-def random_weights(cfg, seed=0, std=0.02):
+def random_weights(cfg, seed=0, std=0.02, normal=None):
+    """Weights of cfg's architecture.  normal(rows, cols, std), when given, supplies
+    each matrix (called once per matrix in the order below); otherwise numpy's PCG64
+    seeded with `seed` draws them."""
     rng = np.random.default_rng(seed)
 
     def mat(rows, cols):
+        if normal is not None:
+            return np.ascontiguousarray(normal(rows, cols, std), dtype=np.float32)
         a = rng.standard_normal((rows, cols), dtype=np.float32)
         a *= np.float32(std)
         return a
