@@ -271,7 +271,25 @@ def cpu_baseline_decode(kv, q_host, threads, budget_s=12.0, max_reps=7):
                          threads=threads)
         times.append(time.perf_counter() - t0)
     step_s = float(np.median(times))
-    return step_s, len(times)
+    return step_s, len(times), times
+
+
+def host_cpu():
+    """The host's CPU model and how many of its logical CPUs this process may run on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return {"model": model, "logical_cpus": os.cpu_count(), "usable_cpus": usable}
 
 
 CHUNKED = dict(heads=32, kv_heads=4, d=64, t=512, start=1536, theta=10000.0, seed=4)
@@ -719,20 +737,25 @@ def main():
 
     # ---------------- CPU baseline (oracle on the host cores, bounded sample)
     if not args.no_cpu:
-        threads = os.cpu_count() or 1
-        step_s, reps = cpu_baseline_decode(kv, q.cpu().numpy(), threads)
+        cpu = host_cpu()
+        threads = min(cpu["usable_cpus"], 16)  # the one-GPU box's CPU share
+        step_s, reps, times = cpu_baseline_decode(kv, q.cpu().numpy(), threads)
         cpu_gbs = bytes_step / step_s / 1e9
         out["cpu_baseline"] = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
                                "sample": f"wick's CPU attention restated in C (AVX2 order), all 24 decode layers at "
                                          f"L=32768 on the host, median of {reps} full steps "
                                          f"({step_s * 1e3:.1f} ms/step; {c['heads']} (token, head) items per layer "
                                          f"over a {threads}-thread pool)",
-                               "ms_per_step": round(step_s * 1e3, 2)}
+                               "ms_per_step": round(step_s * 1e3, 2),
+                               "ms_per_step_min_max": [round(min(times) * 1e3, 2), round(max(times) * 1e3, 2)],
+                               "host_cpu": cpu}
         if threads != 8:
             # wick's default pool clamps at 8 threads (src/engine.rs:53-56)
-            step8, reps8 = cpu_baseline_decode(kv, q.cpu().numpy(), 8)
+            step8, reps8, times8 = cpu_baseline_decode(kv, q.cpu().numpy(), 8)
             out["cpu_baseline"]["threads_8"] = {"value": round(bytes_step / step8 / 1e9, 2), "unit": "GB/s",
-                                                "ms_per_step": round(step8 * 1e3, 2), "reps": reps8}
+                                                "ms_per_step": round(step8 * 1e3, 2), "reps": reps8,
+                                                "ms_per_step_min_max": [round(min(times8) * 1e3, 2),
+                                                                        round(max(times8) * 1e3, 2)]}
     kv.close()
     print(json.dumps(out), flush=True)
 
