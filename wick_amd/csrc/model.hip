@@ -458,14 +458,21 @@ __global__ __launch_bounds__(256) void embed_kernel(const float *__restrict__ em
 
 // step, len (graph-replayed decode loop): the id goes to out[*step + 1], then
 // *step and *len advance to the next forward's token and cache length.
+// embed (greedy decode loop): the workgroup also copies the chosen id's
+// embedding row (hidden floats) to xe, the next forward's input row, in place
+// of that forward's embed_kernel launch.
 __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ x, int n, uint32_t *__restrict__ out,
                                                       int *__restrict__ step, int *__restrict__ len,
-                                                      const float *__restrict__ parts) {
+                                                      const float *__restrict__ parts, const float *__restrict__ embed,
+                                                      float *__restrict__ xe, int hidden) {
     constexpr int U = 8;
     __shared__ float sv[16];
     __shared__ int si[16];
+    __shared__ int sbest;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
+    // x[0] (wick keeps index 0 when it is NaN) is requested with the rest
+    const float x0 = threadIdx.x == 0 ? x[0] : 0.f;
     if (parts) {
         // two pairs per float4
         const int np = argmax_parts(n), np2 = np >> 1;
@@ -537,7 +544,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
     if (threadIdx.x == 0) {
         for (int k = 1; k < 16; k++) arg_better(sv[k], si[k], bv, bi);
         // all values NaN (bi unset) or x[0] NaN: wick keeps index 0
-        if (bi == 0x7fffffff || isnan(x[0])) bi = 0;
+        if (bi == 0x7fffffff || isnan(x0)) bi = 0;
         if (step) {
             const int k = *step;
             out[k + 1] = (uint32_t)bi;
@@ -546,6 +553,13 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
         } else {
             *out = (uint32_t)bi;
         }
+        sbest = bi;
+    }
+    if (embed) {
+        __syncthreads();
+        const f4 *src = reinterpret_cast<const f4 *>(embed + (size_t)sbest * hidden);
+        f4 *dst = reinterpret_cast<f4 *>(xe);
+        for (int c = threadIdx.x; c < hidden / 4; c += blockDim.x) dst[c] = src[c];
     }
 }
 
@@ -672,8 +686,9 @@ hipError_t launch_set_step(int *counters, int step, int len, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float *x, int n, uint32_t *out, hipStream_t s, int *step, int *len, const float *parts) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, x, n, out, step, len, parts);
+hipError_t launch_argmax(const float *x, int n, uint32_t *out, hipStream_t s, int *step, int *len, const float *parts,
+                         const float *embed, float *xe, int hidden) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, x, n, out, step, len, parts, embed, xe, hidden);
     return hipGetLastError();
 }
 

@@ -208,15 +208,18 @@ int product(wick_hip_model *m, int epi, wick::GemvArgs g, const char *what) {
 // token (or of all t when all_logits) go to m->logits.  Queued on m->stream.
 // With counters (t = 1, a step captured for replay) the token is
 // tok_dev[counters[0]] and the cache length counters[1]; start only picks the
-// decode plan, and no buffer may need to grow.
+// decode plan, and no buffer may need to grow.  embedded (t = 1): m->x already
+// holds the token's embedding row (the previous greedy step's argmax wrote it).
 int forward_device(wick_hip_model *m, wick_hip_kv *kv, const uint32_t *tok_dev, int t, int start, bool all_logits,
-                   int *counters = nullptr) {
+                   int *counters = nullptr, bool embedded = false) {
     const wick_hip_model_config &c = m->c;
     const hipStream_t s = m->stream;
     RC_TRY(ensure_activations(m, t));
     RC_TRY(ensure_logits(m, all_logits ? t : 1));
-    hipError_t e = wick::launch_embed(m->embed, tok_dev, m->x, t, c.hidden, s, counters);
-    if (e != hipSuccess) return hip_fail(e, "embed kernel launch");
+    if (!embedded) {
+        hipError_t e = wick::launch_embed(m->embed, tok_dev, m->x, t, c.hidden, s, counters);
+        if (e != hipSuccess) return hip_fail(e, "embed kernel launch");
+    }
     // the gate/up product takes at most kMaxParts partial vectors of up to
     // 2048 floats (its input row in one pass)
     const int group = c.heads / c.kv_heads;
@@ -350,26 +353,31 @@ int upload_ids(wick_hip_model *m, const uint32_t *ids, int n) {
 constexpr int kGraphMinSteps = 24;
 
 // Greedy step i of a decode loop, launched directly: forward of ids[i] at
-// position start + i, argmax into ids[i + 1].
-int decode_step(wick_hip_model *m, wick_hip_kv *kv, int start, int i) {
-    RC_TRY(forward_device(m, kv, m->ids + i, 1, start + i, false));
-    hipError_t e = wick::launch_argmax(m->logits, m->c.vocab, m->ids + i + 1, m->stream, nullptr, nullptr, m->argparts);
+// position start + i (its embedding row already in m->x when `embedded`),
+// argmax into ids[i + 1], whose embedding row the argmax leaves in m->x for
+// the next step.
+int decode_step(wick_hip_model *m, wick_hip_kv *kv, int start, int i, bool embedded) {
+    RC_TRY(forward_device(m, kv, m->ids + i, 1, start + i, false, nullptr, embedded));
+    hipError_t e = wick::launch_argmax(m->logits, m->c.vocab, m->ids + i + 1, m->stream, nullptr, nullptr, m->argparts,
+                                       m->embed, m->x, m->c.hidden);
     if (e != hipSuccess) return hip_fail(e, "argmax launch");
     return WICK_HIP_OK;
 }
 
 // Steps i0..i1-1 (one decode plan) from one captured step replayed as a HIP
 // graph: each replay reads its token index and cache length from
-// m->counters, which its argmax advances.  The graph holds no memset node and
-// is destroyed before returning (it bakes in this call's buffers).
+// m->counters, which its argmax advances; m->x holds ids[i0]'s embedding row
+// (the previous step's argmax wrote it) and each replay's argmax writes the
+// next one.  The graph holds no memset node and is destroyed before returning
+// (it bakes in this call's buffers).
 int decode_replayed(wick_hip_model *m, wick_hip_kv *kv, int start, int i0, int i1) {
     if (!m->counters) HIP_TRY(hipMalloc(&m->counters, 2 * sizeof(int)));
     hipGraph_t graph = nullptr;
     HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-    int rc = forward_device(m, kv, m->ids, 1, start + i0, false, m->counters);
+    int rc = forward_device(m, kv, m->ids, 1, start + i0, false, m->counters, true);
     if (!rc) {
-        hipError_t e =
-            wick::launch_argmax(m->logits, m->c.vocab, m->ids, m->stream, m->counters, m->counters + 1, m->argparts);
+        hipError_t e = wick::launch_argmax(m->logits, m->c.vocab, m->ids, m->stream, m->counters, m->counters + 1,
+                                           m->argparts, m->embed, m->x, m->c.hidden);
         if (e != hipSuccess) rc = hip_fail(e, "argmax launch");
     }
     hipError_t e = hipStreamEndCapture(m->stream, &graph);
@@ -574,11 +582,13 @@ int wick_hip_model_decode(wick_hip_model *m, wick_hip_kv *kv, uint32_t first, in
         const long long plan = wick::decode_plan_key(kv, m->c.heads, start + i + 1);
         int j = i + 1;
         while (j < steps && wick::decode_plan_key(kv, m->c.heads, start + j + 1) == plan) j++;
-        RC_TRY(decode_step(m, kv, start, i));
+        // the loop's first step embeds its token; every argmax leaves the next
+        // token's embedding row in m->x
+        RC_TRY(decode_step(m, kv, start, i, i > 0));
         if (j - (i + 1) >= kGraphMinSteps) {
             RC_TRY(decode_replayed(m, kv, start, i + 1, j));
         } else {
-            for (int k = i + 1; k < j; k++) RC_TRY(decode_step(m, kv, start, k));
+            for (int k = i + 1; k < j; k++) RC_TRY(decode_step(m, kv, start, k, true));
         }
         i = j;
     }

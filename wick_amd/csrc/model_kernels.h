@@ -68,8 +68,11 @@ hipError_t launch_embed(const float *embed, const uint32_t *tokens, float *x, in
 // parts: when non-null, the argmax_parts(n) pairs the kEpiArgmax product wrote
 // for x (pair p: the best of rows kArgmaxRows*p.., as value and the index's
 // bits), which are reduced instead of the n logits.
+// embed, xe: when non-null, embed's row for the chosen id (hidden floats,
+// hidden % 4 == 0) is also copied to xe (the next forward's input row).
 hipError_t launch_argmax(const float *x, int n, uint32_t *out, hipStream_t s, int *step = nullptr, int *len = nullptr,
-                         const float *parts = nullptr);
+                         const float *parts = nullptr, const float *embed = nullptr, float *xe = nullptr,
+                         int hidden = 0);
 // counters[0] = step, counters[1] = len: the state a replayed decode step reads (a kernel,
 // not a host copy, so the values travel with the launch).
 hipError_t launch_set_step(int *counters, int step, int len, hipStream_t s);
