@@ -14,10 +14,10 @@
  * order), the softmax at the temperature, min-p, top-p and the draw from
  * xoshiro256** -- each step in wick's f32 operation order.  Equal logits at the
  * top-k boundary or inside the kept set are ordered by token id (wick's
- * unstable sort leaves their order unspecified).  The exponentials are
- * exp() rounded once to f32; wick calls glibc's expf, which differs from that
- * in the last bit for about 0.06% of arguments, so a probability may differ by
- * 1 ulp (and a draw only if it falls inside that ulp).
+ * unstable sort leaves their order unspecified).  The exponentials follow
+ * glibc's expf (the function wick's f32::exp calls on x86-64 Linux) to the bit
+ * on every f32 input, so probabilities and draws equal wick's for the same
+ * seed and logits.
  *
  * Return codes and wick_hip_last_error() as in wick_hip.h.
  */
