@@ -105,6 +105,58 @@ def test_long_decode_steps_append_llama3_8b_shape():
         assert ok, (layer, s, mabs, mrel)
 
 
+def test_cache_past_the_32_bit_byte_offsets():
+    """Maximum sizes: a head_dim-128 cache of 4,195,328 positions per kv head
+    (2.15 GB per kv head and tensor, past what the lean prefill's 32-bit buffer
+    ranges address, so prefill takes its global-load kernel, and kv head 1's rows
+    start past 2^31 bytes).  A 200-token prefill at the start, then one decode
+    token over 4,195,321 positions (the cache filled with a tiled block of 65,537
+    random rows).  The prefill is checked against the oracle.  Over 4.2 million
+    positions wick's own sequential f32 sums drift past the 2e-5 bar, so the
+    decode is checked against f64 arithmetic instead, which the tiling makes
+    cheap: each of the 65,537 distinct rows enters with its multiplicity."""
+    heads, kvh, d = 4, 2, 128
+    cap = 4195328
+    L = cap - 7
+    rng = np.random.default_rng(17)
+    base_k = rng.standard_normal((65537, kvh * d), dtype=np.float32)
+    base_v = rng.standard_normal((65537, kvh * d), dtype=np.float32)
+    with DeviceKvCache(1, cap, kvh, d) as kv:
+        qp, kp, vp = make_inputs(18, 200, 0, heads, kvh, d)
+        kv.append(0, 0, kp, vp)
+        got = kv.attention(0, heads, qp, 0)
+        ok, mabs, mrel = within_tol(got, ol.attention(qp, kp, vp, 200, 0, heads, kvh, d))
+        print(f"prefill t=200 at capacity {cap}: max abs {mabs:.2e} max rel {mrel:.2e}", flush=True)
+        assert ok, (mabs, mrel)
+        k = np.resize(base_k, (L, kvh * d))
+        v = np.resize(base_v, (L, kvh * d))
+        for c0 in range(0, L, 1 << 20):
+            kv.append(0, c0, k[c0:c0 + (1 << 20)], v[c0:c0 + (1 << 20)])
+        print(f"cache filled to {L} positions", flush=True)
+        q = rng.standard_normal((1, heads * d), dtype=np.float32)
+        got = kv.attention(0, heads, q, L - 1)
+        kr, vr = kv.read(0, L - 3, 3)
+        assert np.array_equal(kr, k[L - 3:]) and np.array_equal(vr, v[L - 3:])
+    # f64 attention over the tiled cache: row r of the block appears mult[r] times
+    P = base_k.shape[0]
+    full, rem = divmod(L, P)
+    mult = np.full(P, float(full))
+    mult[:rem] += 1.0
+    want = np.zeros((1, heads * d))
+    for h in range(heads):
+        j = h // (heads // kvh)
+        kb = base_k[:, j * d:(j + 1) * d].astype(np.float64)
+        vb = base_v[:, j * d:(j + 1) * d].astype(np.float64)
+        sc = kb @ q[0, h * d:(h + 1) * d].astype(np.float64) * float(np.float32(1.0) / np.sqrt(np.float32(d)))
+        w = mult * np.exp(sc - sc.max())
+        want[0, h * d:(h + 1) * d] = (w @ vb) / w.sum()
+    ok, mabs, mrel = within_tol(got, want)
+    print(f"decode over {L} positions against f64: max abs {mabs:.2e} max rel {mrel:.2e}")
+    ref = ol.attention(q, k, v, 1, L - 1, heads, kvh, d)
+    print(f"  (the oracle's f32 sums against f64: max abs {np.abs(ref - want).max():.2e})")
+    assert ok, (mabs, mrel)
+
+
 @pytest.mark.parametrize("L", [1, 2, 15, 16, 17, 63, 64, 65, 129, 1000, 4097])
 @pytest.mark.parametrize("d", [16, 32, 64, 128])
 def test_decode_lengths_and_head_dims(L, d):
