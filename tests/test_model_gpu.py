@@ -268,6 +268,42 @@ def test_fused_projection_and_valu_core_shapes(shape):
             want = om.forward(ost, [tok])
 
 
+@pytest.mark.parametrize("shape", ["kv8-d32", "hidden2304-d64", "kv6-d128-bias-qknorm"])
+def test_unfused_single_token_paths(shape):
+    """One-token forwards whose attention cannot carry the output projection --
+    more than 4 (kv head, head slice) units, or a hidden size above the gate/up
+    prologue's 2048 -- run attention and the o_proj product as two launches.
+    Logits within 1e-4 of the CPU oracle and the same greedy ids over 40 steps,
+    through forward() and through decode() (which replays a captured step)."""
+    hidden, heads, kvh, d, extra = {"kv8-d32": (256, 8, 8, 32, False), "hidden2304-d64": (2304, 4, 2, 64, False),
+                                    "kv6-d128-bias-qknorm": (192, 12, 6, 128, True)}[shape]
+    cfg = Config("qwen3" if extra else "llama", hidden, 384, 2, heads, kvh, d, 300, rms_eps=1e-5,
+                 rope_theta=10000.0, attn_bias=extra, qk_norm=extra)
+    w = random_weights(cfg, seed=41, std=0.05)
+    if extra:
+        w = _bias_and_norms(cfg, w, 42)
+    prompt = [int(x) for x in random_prompt(43, 20, cfg.vocab)]
+    om = ol.OracleModel(cfg, w)
+    ost = om.new_state(64)
+    want = om.forward(ost, prompt)
+    ids = []
+    with DeviceModel(cfg, w) as m:
+        cache = m.new_cache(64)
+        got = m.forward(cache, prompt)
+        for step in range(40):
+            diff = np.abs(got[0] - want[0]).max()
+            assert diff < 1e-4, f"{shape}: step {step} logits differ by {diff}"
+            tok = ol.argmax(want[0])
+            assert int(np.argmax(got[0])) == tok, f"{shape}: step {step}"
+            ids.append(tok)
+            got = m.forward(cache, [tok])
+            want = om.forward(ost, [tok])
+        c2 = m.new_cache(64)
+        first = m.prefill(c2, prompt)
+        assert first == ids[0]
+        assert m.decode(c2, first, 39) == ids[1:]
+
+
 def test_prefill_chunks_of_256():
     """A 300-token prompt runs as chunks of 256 + 44 (src/engine.rs:107, :134)."""
     cfg, w, exp = fixture("qwen3-qknorm-f32")
