@@ -54,6 +54,11 @@ struct wick_hip_kv {
     // staging for the host-pointer entry points
     float *q_dev = nullptr, *att_dev = nullptr, *kst_dev = nullptr, *vst_dev = nullptr;
     size_t q_cap = 0, att_cap = 0, kst_cap = 0;
+    // wick_hip_attention / wick_hip_attend: the call's inputs and output in one
+    // pinned host block and one device block, so each call makes one copy
+    // each way, both DMA from pinned memory
+    float *io_dev = nullptr, *io_host = nullptr;
+    size_t io_cap = 0, io_host_cap = 0;
     // decode split-K workspace (partial softmax states of the chunks)
     float *part = nullptr;
     int ws_units = 0;
@@ -92,6 +97,22 @@ int grow(hipStream_t stream, float **buf, size_t *cap, size_t need, const char *
     hipError_t e = hipMalloc(buf, need * sizeof(float));
     if (e != hipSuccess) return hip_fail(e, what);
     *cap = need;
+    return WICK_HIP_OK;
+}
+
+// The pinned host block and the device block of the host-pointer calls, at
+// least `need` floats each.
+int ensure_io(wick_hip_kv *kv, size_t need) {
+    int rc = grow(kv->stream, &kv->io_dev, &kv->io_cap, need, "hipMalloc(io staging)");
+    if (rc || need <= kv->io_host_cap) return rc;
+    if (kv->io_host) {
+        HIP_TRY(hipStreamSynchronize(kv->stream));  // an earlier copy may still read it
+        (void)hipHostFree(kv->io_host);
+    }
+    kv->io_host = nullptr;
+    kv->io_host_cap = 0;
+    HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&kv->io_host), need * sizeof(float), hipHostMallocDefault));
+    kv->io_host_cap = need;
     return WICK_HIP_OK;
 }
 
@@ -476,9 +497,10 @@ int wick_hip_kv_create(int layers, int capacity, int kv_heads, int head_dim, wic
 void wick_hip_kv_destroy(wick_hip_kv *kv) {
     if (!kv) return;
     if (kv->stream) (void)hipStreamSynchronize(kv->stream);
-    float *bufs[] = {kv->k, kv->v, kv->q_dev, kv->att_dev, kv->kst_dev, kv->vst_dev, kv->part};
+    float *bufs[] = {kv->k, kv->v, kv->q_dev, kv->att_dev, kv->kst_dev, kv->vst_dev, kv->part, kv->io_dev};
     for (float *b : bufs)
         if (b) (void)hipFree(b);
+    if (kv->io_host) (void)hipHostFree(kv->io_host);
     if (kv->rope_cos) (void)hipFree(kv->rope_cos);
     if (kv->rope_sin) (void)hipFree(kv->rope_sin);
     for (auto &p : kv->prep)
@@ -600,13 +622,18 @@ int wick_hip_attention(wick_hip_kv *kv, int layer, int heads, const float *q, in
     if ((rc = check_span(kv, start, t))) return rc;
     if (!q || !att) return fail(WICK_HIP_EINVAL, "null q or att");
     if (heads < 1) return fail(WICK_HIP_EINVAL, "heads must be >= 1");
+    // io blocks: q [n] | att [n]
     const size_t n = (size_t)t * heads * kv->head_dim;
-    if ((rc = grow(kv->stream, &kv->q_dev, &kv->q_cap, n, "hipMalloc(q staging)"))) return rc;
-    if ((rc = grow(kv->stream, &kv->att_dev, &kv->att_cap, n, "hipMalloc(att staging)"))) return rc;
-    HIP_TRY(hipMemcpyAsync(kv->q_dev, q, n * sizeof(float), hipMemcpyHostToDevice, kv->stream));
-    if ((rc = run_attention(kv, layer, heads, kv->q_dev, t, start, kv->att_dev))) return rc;
-    HIP_TRY(hipMemcpyAsync(att, kv->att_dev, n * sizeof(float), hipMemcpyDeviceToHost, kv->stream));
+    if ((rc = ensure_io(kv, 2 * n))) return rc;
+    memcpy(kv->io_host, q, n * sizeof(float));
+    HIP_TRY(hipMemcpyAsync(kv->io_dev, kv->io_host, n * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+    // one token: att straight into the pinned block; a chunk: copied back
+    float *att_out = t == 1 ? kv->io_host + n : kv->io_dev + n;
+    if ((rc = run_attention(kv, layer, heads, kv->io_dev, t, start, att_out))) return rc;
+    if (t > 1)
+        HIP_TRY(hipMemcpyAsync(kv->io_host + n, att_out, n * sizeof(float), hipMemcpyDeviceToHost, kv->stream));
     HIP_TRY(hipStreamSynchronize(kv->stream));
+    memcpy(att, kv->io_host + n, n * sizeof(float));
     return WICK_HIP_OK;
 }
 
@@ -691,23 +718,23 @@ int wick_hip_attend(wick_hip_kv *kv, int layer, int heads, const float *q, const
     if (!q || !k || !v || !att) return fail(WICK_HIP_EINVAL, "null q, k, v or att");
     if (heads < 1 || heads % kv->kv_heads != 0)
         return fail(WICK_HIP_EINVAL, "heads (%d) must be a positive multiple of kv_heads (%d)", heads, kv->kv_heads);
+    // io blocks: q [nq] | k [nk] | v [nk] | att [nq] (each a multiple of head_dim
+    // floats, so every part stays 16-byte aligned)
     const size_t nq = (size_t)t * heads * kv->head_dim, nk = (size_t)t * kv->kv_heads * kv->head_dim;
-    if ((rc = grow(kv->stream, &kv->q_dev, &kv->q_cap, nq, "hipMalloc(q staging)"))) return rc;
-    if ((rc = grow(kv->stream, &kv->att_dev, &kv->att_cap, nq, "hipMalloc(att staging)"))) return rc;
-    if (nk > kv->kst_cap) {
-        size_t ck = kv->kst_cap, cv = kv->kst_cap;
-        kv->kst_cap = 0;
-        if ((rc = grow(kv->stream, &kv->kst_dev, &ck, nk, "hipMalloc(k staging)"))) return rc;
-        if ((rc = grow(kv->stream, &kv->vst_dev, &cv, nk, "hipMalloc(v staging)"))) return rc;
-        kv->kst_cap = nk;
-    }
-    HIP_TRY(hipMemcpyAsync(kv->q_dev, q, nq * sizeof(float), hipMemcpyHostToDevice, kv->stream));
-    HIP_TRY(hipMemcpyAsync(kv->kst_dev, k, nk * sizeof(float), hipMemcpyHostToDevice, kv->stream));
-    HIP_TRY(hipMemcpyAsync(kv->vst_dev, v, nk * sizeof(float), hipMemcpyHostToDevice, kv->stream));
-    if ((rc = wick::attend_model(kv, layer, heads, kv->q_dev, kv->kst_dev, kv->vst_dev, t, start, kv->att_dev)))
-        return rc;
-    HIP_TRY(hipMemcpyAsync(att, kv->att_dev, nq * sizeof(float), hipMemcpyDeviceToHost, kv->stream));
+    if ((rc = ensure_io(kv, 2 * nq + 2 * nk))) return rc;
+    float *h = kv->io_host, *d = kv->io_dev;
+    memcpy(h, q, nq * sizeof(float));
+    memcpy(h + nq, k, nk * sizeof(float));
+    memcpy(h + nq + nk, v, nk * sizeof(float));
+    HIP_TRY(hipMemcpyAsync(d, h, (nq + 2 * nk) * sizeof(float), hipMemcpyHostToDevice, kv->stream));
+    // one token: the kernel writes att straight into the pinned block (a few KB
+    // over the bus, one copy less); a chunk: a device block and one copy back
+    float *att_out = t == 1 ? h + nq + 2 * nk : d + nq + 2 * nk;
+    if ((rc = wick::attend_model(kv, layer, heads, d, d + nq, d + nq + nk, t, start, att_out))) return rc;
+    if (t > 1)
+        HIP_TRY(hipMemcpyAsync(h + nq + 2 * nk, att_out, nq * sizeof(float), hipMemcpyDeviceToHost, kv->stream));
     HIP_TRY(hipStreamSynchronize(kv->stream));
+    memcpy(att, h + nq + 2 * nk, nq * sizeof(float));
     return WICK_HIP_OK;
 }
 
