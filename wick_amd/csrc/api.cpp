@@ -207,6 +207,7 @@ int plan_decode(wick_hip_kv *kv, int layer, int group, int len, const float *q_d
     a->hslices = hslices;
     a->chunk = chunk;
     a->nchunks = nchunks;
+    a->stagger = nchunks > 1 && (long long)units * nchunks >= 2LL * kv->num_cus ? 1 : 0;
     kv->last_grid = units * nchunks;
     return WICK_HIP_OK;
 }

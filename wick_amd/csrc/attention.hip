@@ -848,6 +848,11 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
                 // keeps the K loads ahead of the wait for q
                 __builtin_amdgcn_sched_barrier(0);
                 scale_q();
+                // stagger: the V requests go out in K-arrival order, so the
+                // last bytes of the transfer are V rows whose waves have
+                // their QK products done (config 2: call 11.20 -> 11.11 us;
+                // cache-resident grids, which are latency-bound, lose 0.1 us)
+                if (a.stagger) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 lean_load_global_v<D, TG>(Vh, p0, kend, tail, lane, t);
                 lean_step<D, false, TG>(t, q, p0, tail, kend, g, st.m, st.l, st.o);
                 p0 += step;

@@ -24,6 +24,9 @@ struct DecodeArgs {
     float *att;       // [heads*D]
     float *part;      // partial states, see decode_workspace_floats
     int capacity, len, kv_heads, group, hslices, chunk, nchunks;
+    // a grid of at least two workgroups per CU, streaming from HBM: each wave
+    // requests its first group's V rows only once its K rows have arrived
+    int stagger;
     float scale;
     // Fused input preparation (prep != 0): q is raw; kraw / vraw [kv_heads*D]
     // are the new token's raw k and v, prepared and appended at position len-1
