@@ -189,6 +189,29 @@ def test_generate_matches_oracle(model, case):
     assert got == want
 
 
+@pytest.mark.parametrize("stops", [False, True])
+def test_generate_across_plan_changes(stops):
+    """A long sampled loop: from 150 to 230 positions the decode plan changes at
+    193 (one chunk per kv head -> split-K, with its merge pass) in the middle of
+    the loop.  The ids equal the oracle's Session::generate, with and without a
+    stop list that never matches."""
+    from wick_amd.device_model import DeviceModel
+    from wick_amd.model import Config
+    from wick_amd.synthetic import random_weights
+    cfg = Config("llama", 128, 256, 2, 6, 2, 64, 500, rms_eps=1e-5, rope_theta=10000.0)
+    w = random_weights(cfg, seed=51, std=0.08)
+    scfg = SamplerConfig(temperature=0.8, top_k=20, top_p=0.95, repetition_penalty=1.1, seed=9)
+    rng = np.random.default_rng(52)
+    prompt = [int(t) for t in rng.integers(0, cfg.vocab, 150)]
+    want, want_len = oracle_generate(cfg, w, prompt, 80, scfg, 256)
+    with DeviceModel(cfg, w) as m:
+        cache = m.new_cache(256)
+        with m.new_sampler(scfg) as s:
+            got = m.generate(cache, s, prompt, 80, stops=(cfg.vocab + 7,) if stops else ())
+        assert cache.len == want_len
+    assert got == want
+
+
 def test_generate_stops_and_room():
     from wick_amd.device_model import DeviceModel
     cfg, w = tiny("qwen3-qknorm-f32")
