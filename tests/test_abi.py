@@ -144,3 +144,40 @@ def test_host_mirror_loads_and_reports_errors():
         pass
     with pytest.raises(RuntimeError, match="no HIP device|wick_hip_kv_create"):
         m.new_state(16)
+
+
+def test_c_program_links_every_declared_function(tmp_path):
+    """The headers compile as strict C99 on their own, and a C program that takes the
+    address of every function they declare links against libwick_hip.so and runs
+    (it makes no call, so no device is needed): the declarations and the exported
+    definitions agree for a C linker, not only for ctypes."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    headers = sorted(fn for fn in os.listdir(os.path.join(ROOT, "include")) if fn.endswith(".h"))
+    names = sorted(header_symbols())
+    src = tmp_path / "link_all.c"
+    src.write_text(
+        "".join(f'#include "{h}"\n' for h in headers)
+        + "#include <stdio.h>\n"
+        + "typedef void (*fn_t)(void);\n"
+        + "static const fn_t table[] = {\n"
+        + "".join(f"    (fn_t)&{n},\n" for n in names)
+        + "};\n"
+        + "int main(void) {\n"
+        + "    size_t i, n = sizeof table / sizeof table[0];\n"
+        + "    for (i = 0; i < n; i++)\n"
+        + "        if (!table[i]) return 1;\n"
+        + '    printf("%u\\n", (unsigned)n);\n'
+        + "    return 0;\n"
+        + "}\n")
+    exe = tmp_path / "link_all"
+    libdir = os.path.dirname(_native.HIP_LIB)
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror",
+                    "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe),
+                    "-L", libdir, "-l:" + os.path.basename(_native.HIP_LIB), "-Wl,-rpath," + libdir,
+                    "-Wl,--no-as-needed"], check=True)
+    out = subprocess.run([str(exe)], check=True, stdout=subprocess.PIPE, text=True).stdout
+    assert int(out) == len(names)
