@@ -458,7 +458,12 @@ __device__ __forceinline__ void lean_load_global_k(const float *__restrict__ Kh,
     }
 }
 
-template <int D, int TG = Shape<D>::TG>
+// STREAM: V rows through nontemporal loads (the streaming cache policy).  On
+// long HBM streams -- several groups per wave, or head_dim 128 -- they raise
+// the decode's rate (config 5 per layer 98.5 -> 90.1 us; the Qwen2.5 shape at
+// 512K positions 100.8 -> 90.6 us); on config 2's one group per wave they cost
+// 0.15 us per call, and K through them costs more than it gains everywhere.
+template <int D, int TG = Shape<D>::TG, bool STREAM = false>
 __device__ __forceinline__ void lean_load_global_v(const float *__restrict__ Vh, int p0, int kend, bool clamp,
                                                    int lane, LeanGroup<D, TG> &t) {
     using S = Shape<D>;
@@ -470,16 +475,22 @@ __device__ __forceinline__ void lean_load_global_v(const float *__restrict__ Vh,
         for (int mm = 0; mm < 4; mm++) {
             const float *vr = Vh + (size_t)min(p0 + 16 * u + 4 * g + mm, last) * D + 4 * col;
 #pragma unroll
-            for (int seg = 0; seg < S::NSEG; seg++) t.v[u][mm][seg] = *reinterpret_cast<const f4 *>(vr + 64 * seg);
+            for (int seg = 0; seg < S::NSEG; seg++) {
+                const f4 *src = reinterpret_cast<const f4 *>(vr + 64 * seg);
+                if constexpr (STREAM)
+                    t.v[u][mm][seg] = __builtin_nontemporal_load(src);
+                else
+                    t.v[u][mm][seg] = *src;
+            }
         }
     }
 }
 
-template <int D, int TG = Shape<D>::TG>
+template <int D, int TG = Shape<D>::TG, bool STREAM = false>
 __device__ __forceinline__ void lean_load_global(const float *__restrict__ Kh, const float *__restrict__ Vh, int p0,
                                                  int kend, bool clamp, int lane, LeanGroup<D, TG> &t) {
     lean_load_global_k<D, TG>(Kh, p0, kend, clamp, lane, t);
-    lean_load_global_v<D, TG>(Vh, p0, kend, clamp, lane, t);
+    lean_load_global_v<D, TG, STREAM>(Vh, p0, kend, clamp, lane, t);
 }
 
 template <int D>
@@ -821,21 +832,22 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
         for (int db = 0; db < S::DB; db++) st.o[db] = f4{0.f, 0.f, 0.f, 0.f};
         constexpr int GK = 16 * TG;                 // keys per group
+        constexpr bool kStreamV = D == 128 || PP;  // V through the streaming policy (lean_load_global_v)
         const int wbeg = __builtin_amdgcn_readfirstlane(kbeg + GK * w), step = NW * GK;
         if constexpr (PP) {
             // the next group's loads go out before this group's products
             LeanGroup<D, TG> ta, tb;
             int p0 = wbeg;
-            if (p0 < kend) lean_load_global<D, TG>(Kh, Vh, p0, kend, p0 + GK > kend, lane, ta);
+            if (p0 < kend) lean_load_global<D, TG, kStreamV>(Kh, Vh, p0, kend, p0 + GK > kend, lane, ta);
             __builtin_amdgcn_sched_barrier(0);
             scale_q();
             while (p0 < kend) {
                 const int p1 = p0 + step;
-                if (p1 < kend) lean_load_global<D, TG>(Kh, Vh, p1, kend, p1 + GK > kend, lane, tb);
+                if (p1 < kend) lean_load_global<D, TG, kStreamV>(Kh, Vh, p1, kend, p1 + GK > kend, lane, tb);
                 lean_step<D, false, TG>(ta, q, p0, p0 + GK > kend, kend, g, st.m, st.l, st.o);
                 if (p1 >= kend) break;
                 const int p2 = p1 + step;
-                if (p2 < kend) lean_load_global<D, TG>(Kh, Vh, p2, kend, p2 + GK > kend, lane, ta);
+                if (p2 < kend) lean_load_global<D, TG, kStreamV>(Kh, Vh, p2, kend, p2 + GK > kend, lane, ta);
                 lean_step<D, false, TG>(tb, q, p1, p1 + GK > kend, kend, g, st.m, st.l, st.o);
                 p0 = p2;
             }
@@ -853,14 +865,14 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
                 // their QK products done (config 2: call 11.20 -> 11.11 us;
                 // cache-resident grids, which are latency-bound, lose 0.1 us)
                 if (a.stagger) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                lean_load_global_v<D, TG>(Vh, p0, kend, tail, lane, t);
+                lean_load_global_v<D, TG, kStreamV>(Vh, p0, kend, tail, lane, t);
                 lean_step<D, false, TG>(t, q, p0, tail, kend, g, st.m, st.l, st.o);
                 p0 += step;
             }
             for (; p0 < kend; p0 += step) {
                 LeanGroup<D, TG> t;
                 const bool tail = p0 + GK > kend;
-                lean_load_global<D, TG>(Kh, Vh, p0, kend, tail, lane, t);
+                lean_load_global<D, TG, kStreamV>(Kh, Vh, p0, kend, tail, lane, t);
                 lean_step<D, false, TG>(t, q, p0, tail, kend, g, st.m, st.l, st.o);
             }
         }
