@@ -6,7 +6,8 @@
 //   - read ceiling: one launch that only reads a buffer of the decode layer's
 //     size (no compute, no stores), either each workgroup streaming one
 //     contiguous slice -- the decode kernel's access pattern, a chunk of keys
-//     per workgroup -- or all workgroups striding through the buffer together;
+//     per workgroup -- or all workgroups striding through the buffer together,
+//     through plain or nontemporal (streaming cache policy) loads;
 //   - launch floor: launch to launch of an empty kernel on a given grid.
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -25,6 +26,15 @@ __device__ __forceinline__ void keep(f4 acc, float *sink) {
     if (s == -1.0f) sink[blockIdx.x] = s;
 }
 
+template <bool NT>
+__device__ __forceinline__ f4 ld(const f4 *p) {
+    if constexpr (NT)
+        return __builtin_nontemporal_load(p);
+    else
+        return *p;
+}
+
+template <bool NT>
 __global__ __launch_bounds__(kThreads) void read_slices(const f4 *__restrict__ p, size_t n4, size_t per_wg,
                                                         float *sink) {
     const size_t beg = (size_t)blockIdx.x * per_wg;
@@ -34,14 +44,15 @@ __global__ __launch_bounds__(kThreads) void read_slices(const f4 *__restrict__ p
     for (; i + (kInFlight - 1) * kThreads < end; i += kInFlight * kThreads) {
         f4 x[kInFlight];
 #pragma unroll
-        for (int u = 0; u < kInFlight; u++) x[u] = p[i + u * kThreads];
+        for (int u = 0; u < kInFlight; u++) x[u] = ld<NT>(p + i + u * kThreads);
 #pragma unroll
         for (int u = 0; u < kInFlight; u++) acc += x[u];
     }
-    for (; i < end; i += kThreads) acc += p[i];
+    for (; i < end; i += kThreads) acc += ld<NT>(p + i);
     keep(acc, sink);
 }
 
+template <bool NT>
 __global__ __launch_bounds__(kThreads) void read_strided(const f4 *__restrict__ p, size_t n4, float *sink) {
     const size_t stride = (size_t)gridDim.x * kThreads;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -49,11 +60,11 @@ __global__ __launch_bounds__(kThreads) void read_strided(const f4 *__restrict__ 
     for (; i + (kInFlight - 1) * stride < n4; i += kInFlight * stride) {
         f4 x[kInFlight];
 #pragma unroll
-        for (int u = 0; u < kInFlight; u++) x[u] = p[i + u * stride];
+        for (int u = 0; u < kInFlight; u++) x[u] = ld<NT>(p + i + u * stride);
 #pragma unroll
         for (int u = 0; u < kInFlight; u++) acc += x[u];
     }
-    for (; i < n4; i += stride) acc += p[i];
+    for (; i < n4; i += stride) acc += ld<NT>(p + i);
     keep(acc, sink);
 }
 
@@ -63,18 +74,21 @@ __global__ __launch_bounds__(kThreads) void empty_kernel() {}
 
 extern "C" {
 
-// Read `bytes` (a multiple of 16) at buf on `grid` workgroups; `strided` picks
-// the access pattern.  sink: device array of at least `grid` floats (never
-// written for a buffer of ones).  Asynchronous on `stream`.  0 or a HIP error.
-int wick_probe_read(const void *buf, size_t bytes, int grid, int strided, float *sink, void *stream) {
-    if (!buf || !sink || grid < 1 || bytes % 16 != 0) return (int)hipErrorInvalidValue;
+// Read `bytes` (a multiple of 16) at buf on `grid` workgroups; `mode` bit 0
+// picks the strided access pattern, bit 1 nontemporal loads.  sink: device
+// array of at least `grid` floats (never written for a buffer of ones).
+// Asynchronous on `stream`.  0 or a HIP error.
+int wick_probe_read(const void *buf, size_t bytes, int grid, int mode, float *sink, void *stream) {
+    if (!buf || !sink || grid < 1 || bytes % 16 != 0 || mode < 0 || mode > 3) return (int)hipErrorInvalidValue;
     const size_t n4 = bytes / 16;
     const hipStream_t s = (hipStream_t)stream;
-    if (strided) {
-        hipLaunchKernelGGL(read_strided, dim3(grid), dim3(kThreads), 0, s, (const f4 *)buf, n4, sink);
-    } else {
-        const size_t per_wg = (n4 + grid - 1) / grid;
-        hipLaunchKernelGGL(read_slices, dim3(grid), dim3(kThreads), 0, s, (const f4 *)buf, n4, per_wg, sink);
+    const f4 *p = (const f4 *)buf;
+    const size_t per_wg = (n4 + grid - 1) / grid;
+    switch (mode) {
+    case 0: hipLaunchKernelGGL(read_slices<false>, dim3(grid), dim3(kThreads), 0, s, p, n4, per_wg, sink); break;
+    case 1: hipLaunchKernelGGL(read_strided<false>, dim3(grid), dim3(kThreads), 0, s, p, n4, sink); break;
+    case 2: hipLaunchKernelGGL(read_slices<true>, dim3(grid), dim3(kThreads), 0, s, p, n4, per_wg, sink); break;
+    default: hipLaunchKernelGGL(read_strided<true>, dim3(grid), dim3(kThreads), 0, s, p, n4, sink); break;
     }
     return (int)hipGetLastError();
 }
