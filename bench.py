@@ -703,7 +703,7 @@ def main():
                    "launch": mode, "eager_ms_per_step": round(ms_step_eager, 4),
                    "graph_ms_per_step": None if ms_step_graph is None else round(ms_step_graph, 4)},
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "kernel": "wick::decode_kernel<64, false, false, 4, 2, false, 0> + wick::decode_merge_kernel<64> (one call)", "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": "wick::decode_kernel<64, false, false, 4, 2, false, 0, false> + wick::decode_merge_kernel<64> (one call)", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "traffic_source": traffic_source, "bytes_per_launch": bytes_layer,
                      "us_per_launch": round(ms_launch * 1e3, 3)},
