@@ -189,6 +189,28 @@ def test_decode_many_chunks_all_head_dims(d):
     check(q, k, v, 1, L - 1, 12, 3, d, options=[(_native.OPT_DECODE_CHUNK, 64)])
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_decode_merge_slot_counts(d):
+    """The merge pass loads 16 x NB child slots (NB = 1, 2, 4, 8, 16: the fewest
+    that cover the chunks).  Chunk counts at every edge of those sizes, largest
+    first on one handle, so the workspace slots past each call's chunks hold
+    the previous call's states: they must not leak into the result."""
+    L_max = 64 * 256
+    with DeviceKvCache(1, L_max, 2, d) as kv:
+        kv.set_option(_native.OPT_DECODE_CHUNK, 64)
+        q, k, v = make_inputs(300 + d, 1, L_max - 1, 14, 2, d)
+        kv.append(0, 0, k, v)
+        for n in (256, 255, 129, 128, 65, 64, 33, 32, 17, 16, 2):
+            L = 64 * (n - 1) + 1 + (n % 7)  # n chunks, the last one ragged
+            assert -(-L // 64) == n
+            kk, vv = k[:L], v[:L]
+            got = kv.attention(0, 14, q, L - 1)
+            want = ol.attention(q, kk, vv, 1, L - 1, 14, 2, d)
+            ok, mabs, mrel = within_tol(got, want)
+            print(f"d={d} chunks={n} L={L}: max abs {mabs:.2e} max rel {mrel:.2e}")
+            assert ok, (n, mabs, mrel)
+
+
 def test_decode_repeated_launches_reuse_workspace():
     # the split-K workspace is shared by every call on a handle: many launches
     # in a row, alternating layers, must all be right

@@ -1111,12 +1111,14 @@ __device__ __forceinline__ void merge_pair(P pm, P po, P pl, float &M, float &ac
 // own running max; the 4 groups of each wave then combine pairwise in
 // registers and the 4 wave states in one LDS step.  Child order within a
 // thread and the combine tree are fixed: deterministic for a given nchunks.
-template <int D>
+// NB: child slots per thread, the fewest powers of two that cover nchunks
+// (16 x NB >= nchunks), so a call with few chunks loads no dead slots.
+template <int D, int NB>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
     constexpr int DW = 16;                        // head dims per workgroup
     constexpr int NS = D / DW;                    // slices per column
     constexpr int G = 256 / DW;                   // thread groups over children
-    constexpr int NB = kDecodeMaxChunks / G;      // children per thread
+    static_assert(G * NB <= kDecodeMaxChunks, "child slots past the workspace");
     __shared__ float sm[4][DW], so[4][DW], sl[4][DW];
     const int units = a.kv_heads * a.hslices;
     const int ds = blockIdx.x % NS, head = blockIdx.x / NS;
@@ -1129,10 +1131,10 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
     const int grp = tid / DW, dd = tid % DW;
     const int n = a.nchunks;
 
-    // Every child slot ch < kDecodeMaxChunks lies inside the workspace, so the
-    // loads are unconditional (no exec-mask branch per load delays their
-    // issue) and the children past nchunks -- stale or never written -- are
-    // replaced by a select afterwards.
+    // Every child slot ch < G * NB <= kDecodeMaxChunks lies inside the
+    // workspace, so the loads are unconditional (no exec-mask branch per load
+    // delays their issue) and the children past nchunks -- stale or never
+    // written -- are replaced by a select afterwards.
     float vo[NB], vm[NB], vl[NB];
 #pragma unroll
     for (int u = 0; u < NB; u++) {
@@ -1623,6 +1625,17 @@ void launch_decode_d(const DecodeArgs &a, int grid, hipStream_t s) {
         launch_decode_core<D, false, (D < 128), 4>(a, dim3(grid), s);
 }
 
+template <int D>
+void launch_merge(int nb, dim3 grid, const DecodeArgs &a, hipStream_t s) {
+    switch (nb) {
+    case 1: hipLaunchKernelGGL((decode_merge_kernel<D, 1>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((decode_merge_kernel<D, 2>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((decode_merge_kernel<D, 4>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((decode_merge_kernel<D, 8>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((decode_merge_kernel<D, 16>), grid, dim3(256), 0, s, a); break;
+    }
+}
+
 hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_t s) {
     switch (head_dim) {
     case 16: launch_decode_d<16>(a, grid, s); break;
@@ -1633,8 +1646,16 @@ hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nchunks == 1) return e;
-    const int slices = head_dim / 16;
-    WICK_DISPATCH_D(head_dim, decode_merge_kernel, dim3(a.kv_heads * a.group * slices), dim3(256), 0, s, a);
+    const dim3 mgrid((unsigned)(a.kv_heads * a.group * (head_dim / 16)));
+    // 16 thread groups x NB child slots cover the chunks
+    const int nb = a.nchunks <= 16 ? 1 : a.nchunks <= 32 ? 2 : a.nchunks <= 64 ? 4 : a.nchunks <= 128 ? 8 : 16;
+    switch (head_dim) {
+    case 16: launch_merge<16>(nb, mgrid, a, s); break;
+    case 32: launch_merge<32>(nb, mgrid, a, s); break;
+    case 64: launch_merge<64>(nb, mgrid, a, s); break;
+    case 128: launch_merge<128>(nb, mgrid, a, s); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
