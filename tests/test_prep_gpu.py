@@ -98,6 +98,16 @@ def test_decode_prep_one_wide_chunk(heads, kv_heads):
     run_chunks(heads, kv_heads, 64, [140, 1, 1], 1e4, bias=True, norm=True)
 
 
+@pytest.mark.parametrize("heads,kv_heads", [(3, 3), (6, 3), (9, 3)])
+def test_decode_wave_local_prep_steps(heads, kv_heads):
+    """Groups of 1-3 at head_dim 64 prepare wave-locally in the VALU core: 40
+    single-token steps after 700 positions (split chunks; the new key crosses
+    32-key group boundaries at 704 and 736, so the wave that holds it changes),
+    then a run across the one-chunk / split boundary at 192 positions."""
+    run_chunks(heads, kv_heads, 64, [700] + [1] * 40, 1e4, bias=True, norm=True)
+    run_chunks(heads, kv_heads, 64, [180] + [1] * 20, 1e4, bias=False, norm=False, seed=5)
+
+
 def test_qwen2_shape_bias_chunked_then_decode():
     run_chunks(14, 2, 64, [37, 100, 1, 1], 1e6, bias=True, norm=False)
 
