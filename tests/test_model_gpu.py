@@ -360,3 +360,47 @@ def test_model_errors():
                 m.forward(other, [1])
         cache.len = 0
         assert m.forward(cache, [1, 2, 3]).shape == (1, cfg.vocab)
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_random_config_sweep(case):
+    """Seeded random architectures through the device-resident forward: hidden
+    size, heads, kv heads, head_dim, FFN width, vocabulary, layer count, tied or
+    separate LM head, Qwen2 biases / Qwen3 QK-norm.  Prompt logits within 1e-4
+    of the CPU oracle, then greedy decode() (graph-replayed runs included) equal
+    to the oracle's ids."""
+    rng = np.random.default_rng(700 + case)
+    d = int(rng.choice([16, 32, 64, 128]))
+    kvh = int(rng.integers(1, 5))
+    g = int(rng.choice([1, 2, 3, 4, 6, 8]))
+    heads = kvh * g
+    hidden = int(rng.choice([64, 128, 192, 256, 384]))
+    arch = str(rng.choice(["llama", "qwen2", "qwen3"]))
+    cfg = Config(arch, hidden, int(rng.choice([128, 256, 320])), int(rng.integers(1, 4)), heads, kvh, d,
+                 int(rng.integers(300, 1200)), rms_eps=1e-5, rope_theta=float(rng.choice([1e4, 1e6])),
+                 tie_embeddings=bool(rng.random() < 0.5), attn_bias=arch == "qwen2", qk_norm=arch == "qwen3")
+    w = random_weights(cfg, seed=710 + case, std=0.06)
+    if cfg.attn_bias or cfg.qk_norm:
+        w = _bias_and_norms(cfg, w, 720 + case)
+        for lw in w["layers"]:
+            if not cfg.attn_bias:
+                lw.update(bq=None, bk=None, bv=None)
+            if not cfg.qk_norm:
+                lw.update(q_norm=None, k_norm=None)
+    if not cfg.tie_embeddings:
+        w["lm_head"] = (0.06 * np.random.default_rng(730 + case).standard_normal((cfg.vocab, hidden))).astype(np.float32)
+    n_prompt, n_gen = int(rng.integers(5, 70)), 30
+    prompt = [int(x) for x in random_prompt(740 + case, n_prompt, cfg.vocab)]
+    print(f"case {case}: {arch} hidden={hidden} layers={cfg.layers} Hq={heads} Hkv={kvh} d={d} "
+          f"vocab={cfg.vocab} tied={cfg.tie_embeddings} prompt={n_prompt}", flush=True)
+    cap = n_prompt + n_gen + 4
+    want, want_logits = oracle_greedy(cfg, w, prompt, n_gen, cap)
+    with DeviceModel(cfg, w) as m:
+        cache = m.new_cache(cap)
+        logits = m.forward(cache, prompt)
+        diff = np.abs(logits[0] - want_logits).max()
+        assert diff < 1e-4, f"prompt logits differ by {diff}"
+        cache.len = 0
+        first = m.prefill(cache, prompt)
+        got = [first] + m.decode(cache, first, n_gen - 1)
+    assert got == want
