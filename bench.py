@@ -144,7 +144,7 @@ def time_both(torch, stream, fn, launches_per_step, steps, warmup):
             "hip-graph": time_graph(torch, stream, fn, launches_per_step, steps, warmup)}
 
 
-def measure_ceiling(torch, stream, dev, nbytes, layers, steps, warmup):
+def measure_ceiling(torch, stream, dev, nbytes, layers, steps, warmup, grids=(256, 512, 1024, 2048), floors=True):
     """Practical ceilings of one decode layer's launch on this box, timed like the
     decode itself (one launch per layer over its own buffer, eager and
     graph-replayed): the read-only probe over `layers` distinct buffers of nbytes
@@ -162,7 +162,7 @@ def measure_ceiling(torch, stream, dev, nbytes, layers, steps, warmup):
     sink = torch.ones(4096, device=dev)
     reads = []
     for mode in (0, 1, 2, 3):  # bit 0: strided, bit 1: nontemporal loads
-        for grid in (256, 512, 1024, 2048):
+        for grid in grids:
             def step(grid=grid, mode=mode):
                 for b in bufs:
                     rc = lib.wick_probe_read(b.data_ptr(), nbytes, grid, mode, sink.data_ptr(), s)
@@ -175,7 +175,7 @@ def measure_ceiling(torch, stream, dev, nbytes, layers, steps, warmup):
                           "loads": "nontemporal" if mode & 2 else "plain", "workgroups": grid, "launch": launch,
                           "us_per_launch": round(ms * 1e3, 3), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)})
     floors = {}
-    for grid in (512, 56):
+    for grid in ((512, 56) if floors else ()):
         def empty(grid=grid):
             for _ in range(layers):
                 lib.wick_probe_empty(grid, s)
@@ -187,8 +187,8 @@ def measure_ceiling(torch, stream, dev, nbytes, layers, steps, warmup):
             "reads": reads, "empty_kernel_us": floors,
             "method": f"read-only probe (libwick_probe.so) over {layers} distinct buffers of {nbytes} B (the layer's "
                       f"K+V bytes), one launch per buffer, eager and replayed from a HIP graph (the faster kept), "
-                      f"HIP events on the launch stream; empty kernel launch to launch on 512 and 56 workgroups "
-                      f"both ways"}
+                      f"HIP events on the launch stream" + ("; empty kernel launch to launch on 512 and 56 workgroups "
+                                                            "both ways" if floors else "")}
 
 
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "pmc_traffic_decode64_qwen25_32k.json")
@@ -341,7 +341,7 @@ def measure_prefill(torch, kv_cls, dev, heads, kv_heads, d, T, start, theta, see
     return ms * 1e3, prefill_flops(T, heads, d, start)
 
 
-def measure_long_decode(torch, kv_cls, native, dev, steps):
+def measure_long_decode(torch, kv_cls, native, dev, steps, ceiling=True):
     """32 layers x 65536 positions (16 GiB of K+V), one token per layer per step."""
     c = LONG
     g = Synth(torch, dev, c["seed"])
@@ -392,11 +392,21 @@ def measure_long_decode(torch, kv_cls, native, dev, steps):
             "GBps": round(g32, 1), "pct_of_peak": round(100 * g32 / HBM_PEAK_GBS, 1)}
     steps64 = measure_long_decode_steps(torch, kv, g, inv, dev)
     kv.close()
+    del q, att
+    torch.cuda.empty_cache()
     best = sweep[0]
-    return {"workload": "Llama-3-8B shape (Hq 32 / Hkv 8, d 128), 32 layers x 65536 positions (16 GiB K+V), "
-                        "one query token per layer per step, eager launches",
-            "bytes_per_layer": bytes_layer, "auto": best, "chunk_sweep": sweep, "at_32k_context": at32,
-            "steps_64": steps64}
+    out = {"workload": "Llama-3-8B shape (Hq 32 / Hkv 8, d 128), 32 layers x 65536 positions (16 GiB K+V), "
+                       "one query token per layer per step, eager launches",
+           "bytes_per_layer": bytes_layer, "auto": best, "chunk_sweep": sweep, "at_32k_context": at32,
+           "steps_64": steps64}
+    if ceiling:
+        # the same read-only probe as the headline's ceiling, over this layer's 537 MB
+        cl = measure_ceiling(torch, torch.cuda.current_stream(), dev, 2 * c["L"] * c["kv_heads"] * c["d"] * 4, 4,
+                             steps, 2, grids=(512, 752, 1024, 2048), floors=False)
+        out["ceiling"] = cl
+        out["auto"]["frac_of_ceiling"] = round(best["GBps"] / cl["read_ceiling_GBps"], 4)
+        out["steps_64"]["frac_of_ceiling"] = round(steps64["GBps"] / cl["read_ceiling_GBps"], 4)
+    return out
 
 
 def measure_long_decode_steps(torch, kv, g, inv, dev, nsteps=64):
@@ -741,7 +751,8 @@ def main():
 
     # ---------------- long decode: Llama-3-8B shape, L = 65536, split-K chunk sweep
     if not args.no_long:
-        out["long_decode"] = measure_long_decode(torch, DeviceKvCache, _native, dev, steps=max(4, args.steps // 20))
+        out["long_decode"] = measure_long_decode(torch, DeviceKvCache, _native, dev, steps=max(4, args.steps // 20),
+                                                  ceiling=not args.no_ceiling)
 
     # ---------------- e2e: wick's cmd_bench loop (src/main.rs:223-258)
     if not args.no_e2e:
