@@ -31,6 +31,8 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+from wick_amd.synthetic import DeviceNormals  # noqa: E402  (wick's generator on the device)
+
 HBM_PEAK_GBS = 8000.0
 F32_MFMA_PEAK_TFLOPS = 157.3
 
@@ -65,33 +67,9 @@ def inv_freq_torch(theta, d, dev):
     return torch.tensor([1.0 / theta ** (2.0 * i / d) for i in range(d // 2)], dtype=torch.float32, device=dev)
 
 
-class Synth:
-    """One benchmark configuration's inputs: N(0, 1) times a scale from wick's generator
-    (xoshiro256** seeded through splitmix64 with the configuration's seed,
-    /root/reference/src/sampler.rs:28-55), made normal by Box-Muller, generated on the
-    device by libwick_probe.so's wick_synth_normal.  The i-th tensor asked for reads
-    substream i of the seed's stream (i long jumps), its rows successive jumps."""
-
-    def __init__(self, torch, dev, seed):
-        import ctypes
-        self.torch, self.dev, self.seed, self.count = torch, dev, seed, 0
-        self.lib = ctypes.CDLL(os.path.join(ROOT, "wick_amd", "libwick_probe.so"))
-        self.lib.wick_synth_normal.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_int,
-                                               ctypes.c_ulonglong, ctypes.c_float, ctypes.c_void_p]
-
-    def normal(self, rows, cols, scale=1.0):
-        x = self.torch.empty(rows, cols, device=self.dev)
-        rc = self.lib.wick_synth_normal(x.data_ptr(), self.count, rows, cols, self.seed, scale,
-                                        self.torch.cuda.current_stream().cuda_stream)
-        if rc:
-            raise RuntimeError(f"wick_synth_normal: HIP error {rc}")
-        self.count += 1
-        return x
-
-
 def setup_decode(torch, kv_cls, dev):
     c = DEC
-    g = Synth(torch, dev, c["seed"])
+    g = DeviceNormals(torch, dev, c["seed"])
     inv = inv_freq_torch(c["theta"], c["d"], dev)
     kv = kv_cls(c["layers"], c["L"], c["kv_heads"], c["d"])
     kv.set_stream(torch.cuda.current_stream().cuda_stream)
@@ -144,14 +122,16 @@ def time_both(torch, stream, fn, launches_per_step, steps, warmup):
             "hip-graph": time_graph(torch, stream, fn, launches_per_step, steps, warmup)}
 
 
-def measure_ceiling(torch, stream, dev, nbytes, layers, steps, warmup, grids=(256, 512, 1024, 2048), floors=True):
+def measure_ceiling(torch, stream, dev, nbytes, layers, steps, warmup, grids=(256, 512, 1024, 2048),
+                    floors=(512, 56)):
     """Practical ceilings of one decode layer's launch on this box, timed like the
     decode itself (one launch per layer over its own buffer, eager and
     graph-replayed): the read-only probe over `layers` distinct buffers of nbytes
     (the layer's K+V bytes) at several grids, both access patterns and both load
     policies (plain, nontemporal), and the launch-to-launch floor of an empty
-    kernel on the decode's and the merge's grids.  Each figure is the faster of
-    the two launch methods, so the ceiling is the stricter bound."""
+    kernel on the grids in `floors` (the decode's and the merge's; empty: none).
+    Each figure is the faster of the two launch methods, so the ceiling is the
+    stricter bound."""
     import ctypes
     lib = ctypes.CDLL(os.path.join(ROOT, "wick_amd", "libwick_probe.so"))
     lib.wick_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
@@ -174,21 +154,22 @@ def measure_ceiling(torch, stream, dev, nbytes, layers, steps, warmup, grids=(25
             reads.append({"pattern": "strided" if mode & 1 else "slice per workgroup",
                           "loads": "nontemporal" if mode & 2 else "plain", "workgroups": grid, "launch": launch,
                           "us_per_launch": round(ms * 1e3, 3), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)})
-    floors = {}
-    for grid in ((512, 56) if floors else ()):
+    empties = {}
+    for grid in (floors if floors else ()):
         def empty(grid=grid):
             for _ in range(layers):
                 lib.wick_probe_empty(grid, s)
         t = time_both(torch, stream, empty, layers, steps, warmup)
-        floors[str(grid)] = {k: round(v[1] * 1e3, 3) for k, v in t.items()}
+        empties[str(grid)] = {k: round(v[1] * 1e3, 3) for k, v in t.items()}
     del bufs
     best = max(reads, key=lambda r: r["GBps"])
     return {"read_ceiling_GBps": best["GBps"], "read_ceiling_us": best["us_per_launch"], "best": best,
-            "reads": reads, "empty_kernel_us": floors,
+            "reads": reads, "empty_kernel_us": empties,
             "method": f"read-only probe (libwick_probe.so) over {layers} distinct buffers of {nbytes} B (the layer's "
                       f"K+V bytes), one launch per buffer, eager and replayed from a HIP graph (the faster kept), "
-                      f"HIP events on the launch stream" + ("; empty kernel launch to launch on 512 and 56 workgroups "
-                                                            "both ways" if floors else "")}
+                      f"HIP events on the launch stream" +
+                      (f"; empty kernel launch to launch on {' and '.join(map(str, floors))} workgroups both ways"
+                       if floors else "")}
 
 
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "pmc_traffic_decode64_qwen25_32k.json")
@@ -218,6 +199,16 @@ def traffic_record():
 COPY_MIB = 256
 
 
+def decode_kernel_label(nchunks):
+    """The kernels of one configs[1] decode call as rocprofv3 names them: the split
+    kernel's single-buffered 4-wave instance (every wave takes one group of tiles
+    at 128-key chunks) and the merge instance whose 16 x NB child slots cover
+    nchunks."""
+    nb = next(n for n in (1, 2, 4, 8, 16) if 16 * n >= nchunks)
+    return (f"wick::decode_kernel<64, false, false, 4, 2, false, 0, false> + wick::decode_merge_kernel<64, {nb}> "
+            f"(one call, {nchunks} chunks per kv head)")
+
+
 def pmc_case(torch, kv, q, att, dev):
     """The workload the committed rocprofv3 --pmc summaries are taken on."""
     c = DEC
@@ -238,7 +229,7 @@ def pmc_case_long(torch, kv_cls, dev, layers=4):
     (each 537 MB of K+V, twice the Infinity Cache), one call per layer, then a plain copy
     of known size that calibrates the byte counters."""
     c = LONG
-    g = Synth(torch, dev, c["seed"])
+    g = DeviceNormals(torch, dev, c["seed"])
     inv = inv_freq_torch(c["theta"], c["d"], dev)
     kv = kv_cls(layers, c["L"], c["kv_heads"], c["d"])
     kv.set_stream(torch.cuda.current_stream().cuda_stream)
@@ -268,16 +259,74 @@ def pmc_case_long(torch, kv_cls, dev, layers=4):
           flush=True)
 
 
-def cpu_baseline_decode(kv, q_host, threads, budget_s=12.0, max_reps=7):
-    """wick's CPU attention (the oracle) on the host: decode over all 24 layers, median of reps."""
+# ---------------------------------------------------------------- the CPU checker
+# oracle/liboracle.so (wick's CPU arithmetic restated in C; test infrastructure,
+# loaded through tests/oracle_lib.py) runs here in two roles only, both outside
+# every timed GPU region: the cpu_baseline leg, which times it, and the parity
+# record, where it checks the GPU's outputs on the bench's own inputs.
+
+ATOL, RTOL = 2e-5, 1e-4  # the north star's per-element bound on f32 outputs
+
+
+def oracle_lib():
     sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import numpy as np
     import oracle_lib as ol
+    return ol
+
+
+def tol_record(got, want):
+    """BASELINE's parity columns for one comparison: max abs error, max relative
+    error over elements with |ref| >= 1e-3, and whether every element satisfies
+    |gpu - cpu| <= 2e-5 + 1e-4 |cpu| (and is finite)."""
+    import numpy as np
+    got = np.asarray(got, np.float64).reshape(-1)
+    want = np.asarray(want, np.float64).reshape(-1)
+    err = np.abs(got - want)
+    big = np.abs(want) >= 1e-3
+    return {"max_abs": float(err.max()),
+            "max_rel": float((err[big] / np.abs(want[big])).max()) if big.any() else 0.0,
+            "ok": bool(np.all(err <= ATOL + RTOL * np.abs(want)) and np.all(np.isfinite(got))),
+            "elements": int(got.size)}
+
+
+def merge_records(parts):
+    """One record over several comparisons (worst errors, all ok), parts kept."""
+    out = {"max_abs": max(p["max_abs"] for p in parts.values()),
+           "max_rel": max(p["max_rel"] for p in parts.values()),
+           "ok": all(p["ok"] for p in parts.values())}
+    out.update(parts)
+    return out
+
+
+def parity_decode(decode_layers, q_host, outs, threads):
+    """every layer's decode output at each cache length against the
+    oracle on the same q, K and V (the host copies of the device cache)."""
+    import numpy as np
+    ol = oracle_lib()
     c = DEC
-    layers = []
-    for layer in range(c["layers"]):
-        k, v = kv.read(layer, 0, c["L"])
-        layers.append((k, v))
+    parts = {}
+    for L, att in outs.items():
+        want = np.stack([ol.attention(q_host[layer:layer + 1], decode_layers[layer][0][:L],
+                                      decode_layers[layer][1][:L], 1, L - 1, c["heads"], c["kv_heads"], c["d"],
+                                      threads=threads)[0] for layer in range(c["layers"])])
+        parts[f"L{L}"] = tol_record(att, want)
+    return merge_records(parts)
+
+
+def parity_attention(q, k, v, t, start, heads, kv_heads, d, att, threads):
+    """One layer's attention output against the oracle on the same inputs (host arrays)."""
+    ol = oracle_lib()
+    want = ol.attention(q, k, v, t, start, heads, kv_heads, d, threads=threads)
+    return tol_record(att, want)
+
+
+def cpu_baseline_decode(kv, q_host, threads, budget_s=12.0, max_reps=7, layers=None):
+    """wick's CPU attention (the oracle) on the host: decode over all 24 layers, median of reps."""
+    import numpy as np
+    ol = oracle_lib()
+    c = DEC
+    if layers is None:
+        layers = read_decode_layers(kv)
     times = []
     t_start = time.perf_counter()
     while len(times) < max_reps and (time.perf_counter() - t_start) < budget_s:
@@ -289,6 +338,11 @@ def cpu_baseline_decode(kv, q_host, threads, budget_s=12.0, max_reps=7):
         times.append(time.perf_counter() - t0)
     step_s = float(np.median(times))
     return step_s, len(times), times
+
+
+def read_decode_layers(kv):
+    """Host copies of configs[1]'s 24 cache layers (K, V at 32768 positions each)."""
+    return [kv.read(layer, 0, DEC["L"]) for layer in range(DEC["layers"])]
 
 
 def host_cpu():
@@ -313,9 +367,11 @@ CHUNKED = dict(heads=32, kv_heads=4, d=64, t=512, start=1536, theta=10000.0, see
 LONG = dict(heads=32, kv_heads=8, d=128, layers=32, L=65536, theta=500000.0, seed=5)
 
 
-def measure_prefill(torch, kv_cls, dev, heads, kv_heads, d, T, start, theta, seed, qk_norm, steps):
-    """One layer's attention over T new tokens after `start` cached positions; returns (us, flops)."""
-    g = Synth(torch, dev, seed)
+def measure_prefill(torch, kv_cls, dev, heads, kv_heads, d, T, start, theta, seed, qk_norm, steps, check_threads=0):
+    """One layer's attention over T new tokens after `start` cached positions; returns
+    (us, flops, parity record or None).  check_threads > 0: after the timing, the
+    output is checked against the oracle on the same inputs with that many threads."""
+    g = DeviceNormals(torch, dev, seed)
     inv = inv_freq_torch(theta, d, dev)
     L = start + T
 
@@ -338,13 +394,21 @@ def measure_prefill(torch, kv_cls, dev, heads, kv_heads, d, T, start, theta, see
         kv.attention_device(0, heads, q.data_ptr(), T, start, att.data_ptr())
     ms, _ = time_launches(torch, step, 1, steps, 2)
     kv.close()
-    return ms * 1e3, prefill_flops(T, heads, d, start)
+    rec = None
+    if check_threads:
+        torch.cuda.synchronize()
+        rec = parity_attention(q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), T, start, heads, kv_heads, d,
+                               att.cpu().numpy(), check_threads)
+    return ms * 1e3, prefill_flops(T, heads, d, start), rec
 
 
-def measure_long_decode(torch, kv_cls, native, dev, steps, ceiling=True):
-    """32 layers x 65536 positions (16 GiB of K+V), one token per layer per step."""
+def measure_long_decode(torch, kv_cls, native, dev, steps, ceiling=True, check_threads=0):
+    """32 layers x 65536 positions (16 GiB of K+V), one token per layer per step.
+    check_threads > 0: layer 0's outputs at 65536 and 32768 positions are checked
+    against the oracle (after the timing, before the decode loop rewrites the
+    last 64 rows)."""
     c = LONG
-    g = Synth(torch, dev, c["seed"])
+    g = DeviceNormals(torch, dev, c["seed"])
     inv = inv_freq_torch(c["theta"], c["d"], dev)
     kv = kv_cls(c["layers"], c["L"], c["kv_heads"], c["d"])
     kv.set_stream(torch.cuda.current_stream().cuda_stream)
@@ -390,6 +454,19 @@ def measure_long_decode(torch, kv_cls, native, dev, steps, ceiling=True):
     g32 = b32 / (ms32 * 1e-3) / 1e9
     at32 = {"L": L32, "workgroups": kv.last_grid(), "bytes_per_layer": b32, "us_per_layer": round(ms32 * 1e3, 2),
             "GBps": round(g32, 1), "pct_of_peak": round(100 * g32 / HBM_PEAK_GBS, 1)}
+    parity = None
+    if check_threads:
+        import numpy as np
+        outs = {}
+        for L in (c["L"], L32):
+            kv.attention_device(0, c["heads"], q.data_ptr(), 1, L - 1, att.data_ptr())
+            torch.cuda.synchronize()
+            outs[L] = att[0:1].cpu().numpy()
+        k0, v0 = kv.read(0, 0, c["L"])
+        q0 = q[0:1].cpu().numpy()
+        parity = merge_records({f"L{L}": parity_attention(q0, k0[:L], v0[:L], 1, L - 1, c["heads"], c["kv_heads"],
+                                                          c["d"], o, check_threads) for L, o in outs.items()})
+        del k0, v0
     steps64 = measure_long_decode_steps(torch, kv, g, inv, dev)
     kv.close()
     del q, att
@@ -398,14 +475,21 @@ def measure_long_decode(torch, kv_cls, native, dev, steps, ceiling=True):
     out = {"workload": "Llama-3-8B shape (Hq 32 / Hkv 8, d 128), 32 layers x 65536 positions (16 GiB K+V), "
                        "one query token per layer per step, eager launches",
            "bytes_per_layer": bytes_layer, "auto": best, "chunk_sweep": sweep, "at_32k_context": at32,
-           "steps_64": steps64}
+           "steps_64": steps64, "parity": parity}
     if ceiling:
         # the same read-only probe as the headline's ceiling, over this layer's 537 MB
-        cl = measure_ceiling(torch, torch.cuda.current_stream(), dev, 2 * c["L"] * c["kv_heads"] * c["d"] * 4, 4,
-                             steps, 2, grids=(512, 752, 1024, 2048), floors=False)
+        # and over the 268 MB of the same shape at a 32K context (4 distinct buffers
+        # each, 1 GiB and more in all: past the 256 MB Infinity Cache)
+        kvb = c["kv_heads"] * c["d"] * 4
+        cl = measure_ceiling(torch, torch.cuda.current_stream(), dev, 2 * c["L"] * kvb, 4,
+                             steps, 2, grids=(512, 752, 768, 1024, 2048), floors=())
         out["ceiling"] = cl
         out["auto"]["frac_of_ceiling"] = round(best["GBps"] / cl["read_ceiling_GBps"], 4)
         out["steps_64"]["frac_of_ceiling"] = round(steps64["GBps"] / cl["read_ceiling_GBps"], 4)
+        c32 = measure_ceiling(torch, torch.cuda.current_stream(), dev, 2 * L32 * kvb, 4,
+                              steps, 2, grids=(512, 752, 768, 1024, 2048), floors=())
+        at32["ceiling"] = c32
+        at32["frac_of_ceiling"] = round(g32 / c32["read_ceiling_GBps"], 4)
     return out
 
 
@@ -476,18 +560,67 @@ def measure_long_decode_steps(torch, kv, g, inv, dev, nsteps=64):
     return out
 
 
-def measure_e2e():
+def parity_e2e(cfg, w, prompt, n_gen, ids, logits_first, threads):
+    """configs[0] against the all-CPU oracle forward on the same weights and prompt:
+    the oracle's greedy ids (prefill, then n_gen single-token forwards) against each
+    GPU path's `ids`; the device-resident prefill logits against the oracle's
+    (the reference's 1e-4 bar for a reordered forward, tests/tiny_models.rs:89);
+    and every layer's attention, prefill and each decode step, run on the GPU
+    teacher-forced on the oracle's q and K/V rows (the call site src/model.rs:485),
+    against the oracle's attention output within 2e-5 + 1e-4 |ref|."""
+    import numpy as np
+    from wick_amd import DeviceKvCache
+    ol = oracle_lib()
+    om = ol.OracleModel(cfg, w)
+    T, cap = len(prompt), len(prompt) + n_gen + 8
+    st = om.new_state(cap)
+    logits, qt, at = om.forward(st, prompt, trace=True, threads=threads)
+    logit_diff = float(np.abs(np.asarray(logits_first, np.float64) - logits[0]).max())
+    worst = {"max_abs": 0.0, "max_rel": 0.0, "ok": True, "calls": 0}
+
+    def acc(r):
+        worst["max_abs"] = max(worst["max_abs"], r["max_abs"])
+        worst["max_rel"] = max(worst["max_rel"], r["max_rel"])
+        worst["ok"] = worst["ok"] and r["ok"]
+        worst["calls"] += 1
+    want, margins = [], []
+    with DeviceKvCache(cfg.layers, cap, cfg.kv_heads, cfg.head_dim) as kv:
+        for layer in range(cfg.layers):
+            kv.append(layer, 0, st["k"][layer, :T], st["v"][layer, :T])
+            acc(tol_record(kv.attention(layer, cfg.heads, qt[layer], 0), at[layer]))
+        for s in range(n_gen + 1):
+            top2 = np.partition(logits[0], -2)[-2:]
+            margins.append(float(top2[1] - top2[0]))
+            want.append(ol.argmax(logits[0]))
+            if s == n_gen:
+                break
+            pos = T + s
+            logits, qt, at = om.forward(st, [want[-1]], trace=True, threads=threads)
+            for layer in range(cfg.layers):
+                kv.append(layer, pos, st["k"][layer, pos:pos + 1], st["v"][layer, pos:pos + 1])
+                acc(tol_record(kv.attention(layer, cfg.heads, qt[layer], pos), at[layer]))
+    match = {k: v == want for k, v in ids.items()}
+    return {"greedy_ids_match_oracle": match, "ids": len(want), "min_top2_margin": round(min(margins), 6),
+            "prefill_logits_max_abs": logit_diff, "attention_per_layer": worst,
+            "max_abs": worst["max_abs"], "max_rel": worst["max_rel"],
+            "ok": all(match.values()) and logit_diff < 1e-4 and worst["ok"],
+            "what": f"oracle forward on the same weights and prompt, {T}-token prefill + {n_gen} greedy steps "
+                    f"({threads} threads); attention teacher-forced per layer and step"}
+
+
+def measure_e2e(check_threads=0):
     """configs[0] through wick's cmd_bench loop (src/main.rs:223-258): prefill a 128-token
-    prompt, then 64 greedy single-token forwards; decode tok/s = forwards / wall time."""
+    prompt, then 64 greedy single-token forwards; decode tok/s = forwards / wall time.
+    check_threads > 0: afterwards, both GPU paths' ids and the per-layer attention are
+    checked against the all-CPU oracle (parity_e2e)."""
     import numpy as np
     from wick_amd.device_model import DeviceModel
     from wick_amd.host import HostModel
     import torch
-    from wick_amd.synthetic import random_weights, smollm2_135m, wick_prompt
+    from wick_amd.synthetic import smollm2_135m, wick_generator_weights, wick_prompt
     cfg = smollm2_135m()
     # weights: wick's generator, seed 0, N(0, 0.02); prompt: seed 1, ids uniform over the vocabulary
-    syn = Synth(torch, "cuda", 0)
-    w = random_weights(cfg, normal=lambda rows, cols, std: syn.normal(rows, cols, std).cpu().numpy())
+    w = wick_generator_weights(torch, cfg, seed=0, std=0.02)
     prompt = wick_prompt(1, 128, cfg.vocab)
     n_gen = 64
     # (1) the drop-in: wick's host forward (C++ mirror, projections on the CPU),
@@ -539,9 +672,16 @@ def measure_e2e():
         cache.close()
         if rep and (best_s is None or t1 - t0 < best_s):
             best_s = t1 - t0
+    parity = None
+    if check_threads:
+        cache = dm.new_cache(128 + n_gen + 8)
+        logits_first = dm.forward(cache, prompt)[0]
+        cache.close()
+        parity = parity_e2e(cfg, w, prompt, n_gen, {"device_resident": best[2], "host_forward_gpu_attention": host_ids},
+                            logits_first, check_threads)
     dm.close()
     del w
-    return {"workload": f"random-init SmolLM2-135M architecture, f32, 128-token prompt + {n_gen} greedy "
+    return {"parity": parity,"workload": f"random-init SmolLM2-135M architecture, f32, 128-token prompt + {n_gen} greedy "
                         "tokens (wick's cmd_bench loop: decode tok/s = single-token forwards / wall time)",
             "device_resident": {"prompt_tok_s": round(128 / best[0], 1),
                                 "decode_tok_s": round(n_gen / best[1], 2),
@@ -578,12 +718,19 @@ def time_sampler(vocab, draws=200):
     return round(e0.elapsed_time(e1) * 1e3 / draws, 2)
 
 
+def progress(msg):
+    """One line on stderr as each leg ends (stdout carries only the JSON line)."""
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-parity", action="store_true",
+                    help="skip the parity record (every config's GPU outputs against the CPU oracle)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--e2e-only", action="store_true", help="run only the e2e leg (configs[0]) and print its JSON")
@@ -613,8 +760,11 @@ def main():
     torch.cuda.set_stream(stream)
     c = DEC
 
+    cpu = host_cpu()
+    threads = min(cpu["usable_cpus"], 16)  # the one-GPU box's CPU share
+    check = 0 if args.no_parity else threads
     if args.e2e_only:
-        print(json.dumps(measure_e2e()), flush=True)
+        print(json.dumps(measure_e2e(check)), flush=True)
         return
 
     if args.pmc_case in ("prefill", "prefill512"):
@@ -662,7 +812,7 @@ def main():
     # ways (the faster kept: eager launches of these short calls are bound by the
     # host's issue rate).  Their 24-layer working sets (6.3 MB, 50 MB) fit the
     # 256 MB Infinity Cache, so these rates are effective bandwidth, not HBM alone.
-    lengths = []
+    lengths, decode_outs = [], {}
     for L in (512, 4096, c["L"]):
         def step_l(L=L):
             for layer in range(c["layers"]):
@@ -679,6 +829,10 @@ def main():
                         "GBps": round(gbs, 1), "pct_of_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
                         "workgroups": kv.last_grid(), "launch": launch_l,
                         "served_from": "HBM" if L == c["L"] else "Infinity Cache (24-layer set < 256 MB)"})
+        if check:
+            # every launch of the step wrote the same outputs; keep this length's
+            torch.cuda.synchronize()
+            decode_outs[L] = att.cpu().numpy()
     # HBM bytes per launch measured by the committed rocprofv3 --pmc runs on this
     # same workload (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size).
     # They hold for the kernel source they were measured on: the summary records
@@ -713,24 +867,29 @@ def main():
                    "launch": mode, "eager_ms_per_step": round(ms_step_eager, 4),
                    "graph_ms_per_step": None if ms_step_graph is None else round(ms_step_graph, 4)},
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "kernel": "wick::decode_kernel<64, false, false, 4, 2, false, 0, false> + wick::decode_merge_kernel<64> (one call)", "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": decode_kernel_label(grid // c["kv_heads"]), "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "traffic_source": traffic_source, "bytes_per_launch": bytes_layer,
                      "us_per_launch": round(ms_launch * 1e3, 3)},
         "decode_lengths": lengths,
     }
+    parity = {}
     if ceiling:
         out["roofline"]["ceiling_GBps"] = ceiling["read_ceiling_GBps"]
         out["roofline"]["frac_of_ceiling"] = round(achieved / ceiling["read_ceiling_GBps"], 4)
         out["roofline"]["ceiling"] = ceiling
 
+    progress(f"decode timed ({ms_launch * 1e3:.2f} us per layer call)")
     # ---------------- prefill (configs[2] at T = 512 and 2048; configs[3] chunked)
     if not args.no_prefill:
         pre = {}
         for T in (512, 2048):
             pre[T] = measure_prefill(torch, DeviceKvCache, dev, PRE["heads"], PRE["kv_heads"], PRE["d"], T, 0,
-                                     PRE["theta"], PRE["seed"], qk_norm=True, steps=max(5, args.steps // 10))
-        us2048, fl2048 = pre[2048]
+                                     PRE["theta"], PRE["seed"], qk_norm=True, steps=max(5, args.steps // 10),
+                                     check_threads=check)
+        us2048, fl2048, _ = pre[2048]
+        if check:
+            parity["3"] = merge_records({f"T{T}": pre[T][2] for T in (512, 2048)})
         tf = fl2048 / (us2048 * 1e-6) / 1e12
         out["prefill_tflops"] = round(tf, 2)
         out["roofline_prefill"] = {"bound": "mfma", "kernel": "wick::prefill_lean2_kernel_d128",
@@ -739,32 +898,44 @@ def main():
                                    "flops_per_launch": fl2048, "us_per_launch": round(us2048, 2),
                                    "workload": "causal prefill, Qwen3-0.6B shape (Hq 16 / Hkv 8, d 128), T 2048, "
                                                "QK-norm + RoPE applied, empty cache"}
-        us512, fl512 = pre[512]
+        us512, fl512, _ = pre[512]
         out["prefill_t512"] = {"us_per_launch": round(us512, 2), "tflops": round(fl512 / (us512 * 1e-6) / 1e12, 2)}
         c4 = CHUNKED
-        us4, fl4 = measure_prefill(torch, DeviceKvCache, dev, c4["heads"], c4["kv_heads"], c4["d"], c4["t"],
-                                   c4["start"], c4["theta"], c4["seed"], qk_norm=False, steps=max(5, args.steps // 10))
+        us4, fl4, rec4 = measure_prefill(torch, DeviceKvCache, dev, c4["heads"], c4["kv_heads"], c4["d"], c4["t"],
+                                         c4["start"], c4["theta"], c4["seed"], qk_norm=False,
+                                         steps=max(5, args.steps // 10), check_threads=check)
+        if check:
+            parity["4"] = rec4
         out["chunked_prefill"] = {"workload": "TinyLlama-1.1B shape (Hq 32 / Hkv 4, d 64), 512 tokens appended "
                                               "onto 1536 cached positions, per layer",
                                   "us_per_layer": round(us4, 2), "tflops": round(fl4 / (us4 * 1e-6) / 1e12, 2),
                                   "flops_per_layer": fl4}
 
+    progress("prefill legs done")
     # ---------------- long decode: Llama-3-8B shape, L = 65536, split-K chunk sweep
     if not args.no_long:
         out["long_decode"] = measure_long_decode(torch, DeviceKvCache, _native, dev, steps=max(4, args.steps // 20),
-                                                  ceiling=not args.no_ceiling)
+                                                  ceiling=not args.no_ceiling, check_threads=check)
+        if check:
+            parity["5"] = out["long_decode"]["parity"]
 
+    progress("long decode done")
     # ---------------- e2e: wick's cmd_bench loop (src/main.rs:223-258)
     if not args.no_e2e:
-        e2e = measure_e2e()
+        e2e = measure_e2e(check)
+        if check:
+            parity["1"] = e2e["parity"]
         out["e2e_decode_tok_s"] = e2e["device_resident"]["decode_tok_s"]
         out["e2e"] = e2e
 
-    # ---------------- CPU baseline (oracle on the host cores, bounded sample)
+    progress("e2e done")
+    # ---------------- the CPU leg: the oracle on the host cores (bounded sample), and
+    # configs[1]'s parity on the same host copies of the 24 layers
+    decode_layers = read_decode_layers(kv) if (check or not args.no_cpu) else None
+    if check:
+        parity["2"] = parity_decode(decode_layers, q.cpu().numpy(), decode_outs, threads)
     if not args.no_cpu:
-        cpu = host_cpu()
-        threads = min(cpu["usable_cpus"], 16)  # the one-GPU box's CPU share
-        step_s, reps, times = cpu_baseline_decode(kv, q.cpu().numpy(), threads)
+        step_s, reps, times = cpu_baseline_decode(kv, q.cpu().numpy(), threads, layers=decode_layers)
         cpu_gbs = bytes_step / step_s / 1e9
         out["cpu_baseline"] = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
                                "sample": f"wick's CPU attention restated in C (AVX2 order), all 24 decode layers at "
@@ -776,11 +947,18 @@ def main():
                                "host_cpu": cpu}
         if threads != 8:
             # wick's default pool clamps at 8 threads (src/engine.rs:53-56)
-            step8, reps8, times8 = cpu_baseline_decode(kv, q.cpu().numpy(), 8)
+            step8, reps8, times8 = cpu_baseline_decode(kv, q.cpu().numpy(), 8, layers=decode_layers)
             out["cpu_baseline"]["threads_8"] = {"value": round(bytes_step / step8 / 1e9, 2), "unit": "GB/s",
                                                 "ms_per_step": round(step8 * 1e3, 2), "reps": reps8,
                                                 "ms_per_step_min_max": [round(min(times8) * 1e3, 2),
                                                                         round(max(times8) * 1e3, 2)]}
+    del decode_layers
+    if check:
+        out["parity"] = {k: parity[k] for k in sorted(parity)}
+        out["parity"]["ok"] = all(r["ok"] for r in parity.values())
+        out["parity"]["bound"] = ("per element |gpu - cpu| <= 2e-5 + 1e-4 |cpu|; max_rel over |cpu| >= 1e-3; "
+                                  "cpu = the oracle (wick's CPU attention restated in C, AVX2 order) on the bench's "
+                                  "own inputs; config 1: greedy ids identical and prefill logits within 1e-4")
     kv.close()
     print(json.dumps(out), flush=True)
 

@@ -138,13 +138,18 @@ int wick_hip_kv_set_stream(wick_hip_kv *kv, void *stream);
 int wick_hip_kv_synchronize(wick_hip_kv *kv);
 
 /* Tuning knobs. */
-#define WICK_HIP_OPT_DECODE_CHUNK 1 /* positions per decode workgroup (multiple of 64; 0 = automatic) */
-#define WICK_HIP_OPT_PREFILL_PAIRING 2 /* one-wave-per-block prefill: 1 = pair row blocks (b, n-1-b); 0 = never; -1 = automatic */
-#define WICK_HIP_OPT_PREFILL_SPLIT 3   /* 1 = workgroup per row block, keys split across its 4 waves (default); 0 = one wave per block */
+#define WICK_HIP_OPT_DECODE_CHUNK 1 /* positions per decode workgroup (a multiple of 16, at least 64; 0 = automatic) */
 int wick_hip_kv_set_option(wick_hip_kv *kv, int option, int value);
 
 /* Number of workgroups the last attention call launched (for measurement). */
 int wick_hip_kv_last_grid(const wick_hip_kv *kv);
+
+/* Bytes of staging and decode workspace the handle has allocated so far, beyond
+ * its K/V cache and RoPE / preparation tables (device and pinned host memory;
+ * grown on demand by the allocating entry points, never by
+ * wick_hip_attention_device_noalloc).  No counterpart in the reference: for
+ * tests and inspection. */
+long long wick_hip_kv_scratch_bytes(const wick_hip_kv *kv);
 
 #ifdef __cplusplus
 }

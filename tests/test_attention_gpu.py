@@ -61,6 +61,45 @@ def test_decode_llama3_8b_shape_65536():
     check(q, k, v, 1, 65535, 32, 8, 128)
 
 
+def test_decode_llama3_8b_shape_32768():
+    """The Llama-3-8B shape at the headline's 32K context.  The automatic plan
+    sizes chunks in 16-key steps to fill one resident round (94 chunks of 352
+    keys on a 256-CU MI355X), so most chunks are not a whole number of the
+    kernel's 64-key rounds of tile groups."""
+    L = 32768
+    q, k, v = make_inputs(55, 1, L - 1, 32, 8, 128, theta=500000.0)
+    with DeviceKvCache(1, L, 8, 128) as kv:
+        kv.append(0, 0, k, v)
+        got = kv.attention(0, 32, q, L - 1)
+        grid = kv.last_grid()
+    want = ol.attention(q, k, v, 1, L - 1, 32, 8, 128)
+    ok, mabs, mrel = within_tol(got, want)
+    print(f"L={L}: {grid} workgroups, max abs {mabs:.2e} max rel {mrel:.2e}")
+    assert ok, (mabs, mrel)
+    assert grid % 8 == 0
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("chunk", [80, 208, 336, 688])
+def test_decode_chunks_in_16_key_steps(chunk, d):
+    """Chunks that are multiples of 16 keys but not of the 32-key tile groups
+    (head_dim 64) or of a workgroup's 4 groups: the last group of a wave's range,
+    and whole waves, fall past the chunk's end.  The context leaves the last chunk
+    ragged."""
+    L = 37 * chunk - 5
+    q, k, v = make_inputs(chunk + d, 1, L - 1, 14, 2, d)
+    check(q, k, v, 1, L - 1, 14, 2, d, options=[(_native.OPT_DECODE_CHUNK, chunk)])
+
+
+def test_decode_chunk_option_values():
+    with DeviceKvCache(1, 64, 2, 64) as kv:
+        for bad in (-16, 16, 48, 100, 72):
+            with pytest.raises(_native.WickHipError):
+                kv.set_option(_native.OPT_DECODE_CHUNK, bad)
+        for good in (0, 64, 80, 4096):
+            kv.set_option(_native.OPT_DECODE_CHUNK, good)
+
+
 def test_long_decode_steps_append_llama3_8b_shape():
     """configs[4] as a decode loop (Session::step -> Model::forward,
     /root/reference/src/engine.rs:142-145, src/model.rs:481-485): the cache holds
@@ -294,21 +333,18 @@ def test_prefill_ragged(t, start, d):
     check(q, k, v, t, start, 4, 2, d)
 
 
-@pytest.mark.parametrize("split,pairing", [(0, 0), (0, 1), (1, -1)])
 @pytest.mark.parametrize("heads,kv_heads", [(9, 3), (14, 2), (32, 4), (6, 6)])
-def test_prefill_schedules_and_groups(split, pairing, heads, kv_heads):
+def test_prefill_groups(heads, kv_heads):
     t, start = 300, 20
-    q, k, v = make_inputs(heads + pairing, t, start, heads, kv_heads, 64)
-    check(q, k, v, t, start, heads, kv_heads, 64,
-          options=[(_native.OPT_PREFILL_SPLIT, split), (_native.OPT_PREFILL_PAIRING, pairing)])
+    q, k, v = make_inputs(heads + 1, t, start, heads, kv_heads, 64)
+    check(q, k, v, t, start, heads, kv_heads, 64)
 
 
-@pytest.mark.parametrize("split", [0, 1])
 @pytest.mark.parametrize("d", [16, 32, 64, 128])
-def test_prefill_schedules_agree_within_tolerance(split, d):
+def test_prefill_on_a_prefix_all_head_dims(d):
     t, start = 77, 200
-    q, k, v = make_inputs(d * 3 + split, t, start, 8, 2, d)
-    check(q, k, v, t, start, 8, 2, d, options=[(_native.OPT_PREFILL_SPLIT, split)])
+    q, k, v = make_inputs(d * 3 + 1, t, start, 8, 2, d)
+    check(q, k, v, t, start, 8, 2, d)
 
 
 @pytest.mark.parametrize("t,start,heads,kv_heads,d", [(1032, 37, 16, 8, 128), (516, 0, 32, 8, 128),

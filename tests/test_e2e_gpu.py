@@ -13,7 +13,7 @@ from util import within_tol
 from wick_amd import DeviceKvCache
 from wick_amd.host import HostModel
 from wick_amd.model import Config, load_weights
-from wick_amd.synthetic import random_prompt, random_weights, smollm2_135m
+from wick_amd.synthetic import random_prompt, random_weights, smollm2_135m, wick_generator_weights, wick_prompt
 
 pytestmark = pytest.mark.gpu
 
@@ -109,6 +109,48 @@ def test_smollm2_135m_greedy_ids_match_cpu():
     got, margins = greedy(hm, hm.new_state(128 + 64 + 8), prompt, 64)
     print("min top-2 margin over the 64 steps:", min(margins))
     assert got == want
+
+
+def test_smollm2_135m_on_the_configs_own_inputs():
+    """configs[0] on the inputs bench.py runs: weights from wick's generator with
+    seed 0 (N(0, 0.02), /root/reference/src/sampler.rs:28-61, drawn on the device
+    by libwick_probe.so and copied to the host), the prompt from seed 1 (128 ids,
+    next_u64() % vocab), then 64 greedy steps (the cmd_bench loop,
+    /root/reference/src/main.rs:242-246).  The device-resident forward's and the
+    host forward's 65 ids must equal the all-CPU oracle's, and the device
+    prefill logits must lie within 1e-4 of the oracle's."""
+    import torch
+    from wick_amd.device_model import DeviceModel
+    cfg = smollm2_135m()
+    w = wick_generator_weights(torch, cfg, seed=0, std=0.02)
+    prompt = wick_prompt(1, 128, cfg.vocab)
+    cap = 128 + 64 + 8
+    om = ol.OracleModel(cfg, w)
+    ost = om.new_state(cap)
+    logits = om.forward(ost, prompt)
+    first_logits = logits[0].copy()
+    want, margins = [], []
+    for s in range(65):
+        top2 = np.partition(logits[0], -2)[-2:]
+        margins.append(float(top2[1] - top2[0]))
+        want.append(ol.argmax(logits[0]))
+        if s < 64:
+            logits = om.forward(ost, [want[-1]])
+    print(f"min top-2 margin over the 65 ids: {min(margins):.3e}")
+    with DeviceModel(cfg, w) as m:
+        cache = m.new_cache(cap)
+        got_logits = m.forward(cache, prompt)[0]
+        cache.len = 0
+        first = m.prefill(cache, prompt)
+        dev_ids = [first] + m.decode(cache, first, 64)
+    d = float(np.abs(got_logits - first_logits).max())
+    print(f"prefill logits: max |gpu - cpu| = {d:.2e}")
+    assert d < 1e-4
+    assert dev_ids == want
+    hm = HostModel(cfg, w)
+    host_ids, _ = greedy(hm, hm.new_state(cap), prompt, 65)
+    hm.close()
+    assert host_ids == want
 
 
 def test_smollm2_135m_attention_teacher_forced():

@@ -268,6 +268,40 @@ def test_fused_projection_and_valu_core_shapes(shape):
             want = om.forward(ost, [tok])
 
 
+@pytest.mark.parametrize("chunk", [320, 512])
+def test_fixed_decode_chunk_past_the_fused_limit(chunk):
+    """A decode chunk option above the fused attention + output projection's 256
+    keys, at contexts that fit one chunk: every one-token forward must take the
+    separate attention and o_proj launches (the fused launcher refuses such a
+    plan).  SmolLM2's shape over 20..60 positions: logits within 1e-4 of the CPU
+    oracle and the same greedy ids, through forward() and decode()."""
+    cfg = smollm2_135m()
+    cfg.layers = 2
+    w = random_weights(cfg, seed=51)
+    prompt = [int(x) for x in random_prompt(52, 20, cfg.vocab)]
+    om = ol.OracleModel(cfg, w)
+    ost = om.new_state(64)
+    want = om.forward(ost, prompt)
+    ids = []
+    with DeviceModel(cfg, w) as m:
+        cache = m.new_cache(64)
+        cache.set_option(_native.OPT_DECODE_CHUNK, chunk)
+        got = m.forward(cache, prompt)
+        for step in range(40):
+            diff = np.abs(got[0] - want[0]).max()
+            assert diff < 1e-4, f"chunk {chunk}: step {step} logits differ by {diff}"
+            tok = ol.argmax(want[0])
+            assert int(np.argmax(got[0])) == tok, f"chunk {chunk}: step {step}"
+            ids.append(tok)
+            got = m.forward(cache, [tok])
+            want = om.forward(ost, [tok])
+        c2 = m.new_cache(64)
+        c2.set_option(_native.OPT_DECODE_CHUNK, chunk)
+        first = m.prefill(c2, prompt)
+        assert first == ids[0]
+        assert m.decode(c2, first, 39) == ids[1:]
+
+
 @pytest.mark.parametrize("shape", ["kv8-d32", "hidden2304-d64", "kv6-d128-bias-qknorm"])
 def test_unfused_single_token_paths(shape):
     """One-token forwards whose attention cannot carry the output projection --

@@ -70,6 +70,63 @@ def test_noalloc_matches_the_allocating_entry_point_on_calls_in_a_row():
             _check(f"qwen2.5 {Ls}", kv, qs, k, v, 1, Ls, heads, kv_heads, d)
 
 
+def test_noalloc_first_on_a_fresh_handle_allocates_nothing():
+    """The no-allocation entry point called first on a fresh handle, its inputs
+    appended from device arrays (no staging): the handle's staging and workspace
+    stay empty and the GPU's free memory unchanged over decode calls at 32K, 4096
+    and 100 positions and a 100-token chunk.  The allocating entry point on the
+    same handle afterwards grows its workspace and gives the same bits."""
+    import torch
+    heads, kv_heads, d, L = 14, 2, 64, 32768
+    q, k, v = _inputs(12, 1, L, heads, kv_heads, d, 1e6)
+    qc = _inputs(13, 100, 300, heads, kv_heads, d, 1e6)[0]
+    kd, vd = torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda()
+    qd, qcd = torch.from_numpy(q).cuda(), torch.from_numpy(qc).cuda()
+    att = torch.full_like(qd, float("nan"))
+    attc = torch.full_like(qcd, float("nan"))
+    # one stream for everything, first used by another handle running the same
+    # kernels, so the runtime's lazily created per-stream and per-kernel state
+    # exists before the free memory is read
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with DeviceKvCache(1, L, kv_heads, d) as warm:
+        warm.set_stream(stream.cuda_stream)
+        warm.append_device(0, 0, L, kd.data_ptr(), vd.data_ptr())
+        for Ls in (L, 4096, 100):
+            warm.attention_device_noalloc(0, heads, qd.data_ptr(), 1, Ls - 1, att.data_ptr())
+        warm.attention_device_noalloc(0, heads, qcd.data_ptr(), 100, 200, attc.data_ptr())
+        warm.synchronize()
+    with DeviceKvCache(1, L, kv_heads, d) as kv:
+        kv.set_stream(stream.cuda_stream)
+        kv.append_device(0, 0, L, kd.data_ptr(), vd.data_ptr())
+        kv.synchronize()
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        assert kv.scratch_bytes() == 0
+        outs = {}
+        for Ls in (L, 4096, 100):
+            kv.attention_device_noalloc(0, heads, qd.data_ptr(), 1, Ls - 1, att.data_ptr())
+            kv.synchronize()
+            outs[Ls] = att.cpu().numpy()
+        kv.attention_device_noalloc(0, heads, qcd.data_ptr(), 100, 200, attc.data_ptr())
+        kv.synchronize()
+        outc = attc.cpu().numpy()
+        assert kv.scratch_bytes() == 0, "the no-allocation entry point grew the handle's buffers"
+        assert torch.cuda.mem_get_info()[0] == free0, "device memory was allocated"
+        for Ls, got in outs.items():
+            want = ol.attention(q, k[:Ls], v[:Ls], 1, Ls - 1, heads, kv_heads, d)
+            ok, mabs, mrel = within_tol(got, want)
+            print(f"fresh handle, no-alloc first: L={Ls} max abs {mabs:.2e} max rel {mrel:.2e}", flush=True)
+            assert ok, (Ls, mabs, mrel)
+        wantc = ol.attention(qc, k[:300], v[:300], 100, 200, heads, kv_heads, d)
+        assert within_tol(outc, wantc)[0]
+        ref = torch.full_like(qd, float("nan"))
+        kv.attention_device(0, heads, qd.data_ptr(), 1, L - 1, ref.data_ptr())
+        kv.synchronize()
+        assert kv.scratch_bytes() > 0
+        assert np.array_equal(ref.cpu().numpy().view(np.uint32), outs[L].view(np.uint32))
+
+
 def test_noalloc_prefill_uses_no_workspace_and_matches():
     heads, kv_heads, d, t, L = 32, 4, 64, 100, 300
     q, k, v = _inputs(4, t, L, heads, kv_heads, d, 10000.0)

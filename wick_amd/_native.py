@@ -17,8 +17,6 @@ ENOMEM = -3
 EDEVICE = -4
 
 OPT_DECODE_CHUNK = 1
-OPT_PREFILL_PAIRING = 2
-OPT_PREFILL_SPLIT = 3
 
 # Every symbol include/*.h declares, with its ctypes signature.
 _P = ctypes.c_void_p
@@ -38,6 +36,7 @@ SIGNATURES = {
     "wick_hip_kv_synchronize": (_I, [_P]),
     "wick_hip_kv_set_option": (_I, [_P, _I, _I]),
     "wick_hip_kv_last_grid": (_I, [_P]),
+    "wick_hip_kv_scratch_bytes": (ctypes.c_longlong, [_P]),
     "wick_hip_kv_set_rope": (_I, [_P, _P]),
     "wick_hip_kv_set_prep": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, ctypes.c_float]),
     "wick_hip_attend": (_I, [_P, _I, _I, _P, _P, _P, _I, _I, _P]),

@@ -65,7 +65,7 @@ struct wick_hip_kv {
     // whether the static workspace's address was found on this device
     hipError_t static_rc = hipErrorNotInitialized;
     // options
-    int decode_chunk = 0, pairing = -1, prefill_split = 1, last_grid = 0;
+    int decode_chunk = 0, last_grid = 0;
     int decode_blocks_per_cu = 1, prefill_blocks_per_cu = 1, prefill2_blocks_per_cu = 1;
     // input preparation (wick_hip_kv_set_rope / wick_hip_kv_set_prep)
     float *rope_cos = nullptr, *rope_sin = nullptr;  // [capacity][head_dim/2]
@@ -154,22 +154,29 @@ int check_span(const wick_hip_kv *kv, int start, int t) {
 // Chunk size and count of a decode call over len positions for `units`
 // (kv head x 16-head slice) workgroup rows.
 void plan_chunks(const wick_hip_kv *kv, int units, int len, int *chunk_out, int *nchunks_out) {
-    int chunk = kv->decode_chunk;
+    int chunk = kv->decode_chunk, quantum = 16;
     if (chunk <= 0 && len <= wick::kDecodeSingleChunkMax) {
         // Short context: one workgroup per unit and no merge pass.  Its
         // waves (8 at head_dim <= 64, else 4) take at most two tile groups
         // each, which costs less than the second launch a split needs.
+        // Whole 64-key chunks, so that a decode loop keeps one launch plan
+        // (and one captured graph) over 64 consecutive lengths.
         chunk = len;
+        quantum = 64;
     } else if (chunk <= 0) {
         // One resident round: as many chunks as the GPU holds decode
         // workgroups at once, each streaming one long contiguous range.
+        // Chunks in 16-key steps let the grid fill the round: the
+        // Llama-3-8B shape at 32768 positions takes 94 chunks of 352 keys
+        // (752 of 768 resident workgroups) where 64-key steps gave 86 of 384
+        // (688).
         const int resident = kv->num_cus * kv->decode_blocks_per_cu;
         const int target = std::max(1, resident / units);
         chunk = (len + target - 1) / target;
     }
-    chunk = std::max(64, (chunk + 63) / 64 * 64);
+    chunk = std::max(64, (chunk + quantum - 1) / quantum * quantum);
     const int min_chunk = (len + wick::kDecodeMaxChunks - 1) / wick::kDecodeMaxChunks;
-    if (chunk < min_chunk) chunk = (min_chunk + 63) / 64 * 64;
+    if (chunk < min_chunk) chunk = (min_chunk + 15) / 16 * 16;
     *chunk_out = chunk;
     *nchunks_out = (len + chunk - 1) / chunk;
 }
@@ -241,21 +248,11 @@ int run_attention(wick_hip_kv *kv, int layer, int heads, const float *q_dev, int
     a.kv_heads = kv->kv_heads;
     a.group = group;
     a.nblocks = (t * group + wick::kTileRows - 1) / wick::kTileRows;
-    int paired = kv->pairing;
-    if (paired < 0) {
-        // Pair causal row blocks when the triangle dominates (short prefix) and
-        // there are enough blocks to keep every SIMD busy after halving.
-        const long long waves_unpaired = (long long)a.nblocks * kv->kv_heads;
-        paired = (start < t && waves_unpaired >= 2LL * 4 * kv->num_cus) ? 1 : 0;
-    }
-    a.paired = paired;
-    a.items = paired ? (a.nblocks + 1) / 2 : a.nblocks;
-    a.split = kv->prefill_split;
     // Two row blocks per workgroup share each loaded tile, where that grid
     // still gives every CU two workgroups; zigzag pairing where the launched
     // grid is resident at once.
     const long long grid1 = (long long)a.kv_heads * a.nblocks, grid2 = (long long)a.kv_heads * ((a.nblocks + 1) / 2);
-    a.rows32 = wick::prefill_has_rows32(D, kv->capacity, a.split) && grid2 >= 2LL * kv->num_cus ? 1 : 0;
+    a.rows32 = wick::prefill_has_rows32(D, kv->capacity) && grid2 >= 2LL * kv->num_cus ? 1 : 0;
     a.zigzag = (a.rows32 ? grid2 : grid1) <=
                        (long long)kv->num_cus * (a.rows32 ? kv->prefill2_blocks_per_cu : kv->prefill_blocks_per_cu)
                    ? 1
@@ -399,7 +396,7 @@ int attend_model_oproj(wick_hip_kv *kv, int layer, int heads, float *q_dev, cons
     const int hslices = (group + wick::kTileRows - 1) / wick::kTileRows;
     int chunk, nchunks;
     plan_chunks(kv, kv->kv_heads * hslices, start + 1, &chunk, &nchunks);
-    if (!wick::decode_oproj_supported(kv->head_dim, group, nchunks)) return 1;
+    if (!wick::decode_oproj_supported(kv->head_dim, group, nchunks, chunk)) return 1;
     PrepConsts c;
     if ((rc = prep_consts(kv, layer, heads, &c))) return rc;
     wick::DecodeArgs a{};
@@ -526,16 +523,9 @@ int wick_hip_kv_set_option(wick_hip_kv *kv, int option, int value) {
     if (!kv) return fail(WICK_HIP_EINVAL, "null cache handle");
     switch (option) {
     case WICK_HIP_OPT_DECODE_CHUNK:
-        if (value < 0 || value % 64 != 0) return fail(WICK_HIP_EINVAL, "decode chunk must be 0 or a multiple of 64");
+        if (value != 0 && (value < 64 || value % 16 != 0))
+            return fail(WICK_HIP_EINVAL, "decode chunk must be 0 or a multiple of 16 of at least 64 (got %d)", value);
         kv->decode_chunk = value;
-        return WICK_HIP_OK;
-    case WICK_HIP_OPT_PREFILL_PAIRING:
-        if (value < -1 || value > 1) return fail(WICK_HIP_EINVAL, "pairing must be -1, 0 or 1");
-        kv->pairing = value;
-        return WICK_HIP_OK;
-    case WICK_HIP_OPT_PREFILL_SPLIT:
-        if (value < 0 || value > 1) return fail(WICK_HIP_EINVAL, "prefill split must be 0 or 1");
-        kv->prefill_split = value;
         return WICK_HIP_OK;
     default:
         return fail(WICK_HIP_EINVAL, "unknown option %d", option);
@@ -543,6 +533,13 @@ int wick_hip_kv_set_option(wick_hip_kv *kv, int option, int value) {
 }
 
 int wick_hip_kv_last_grid(const wick_hip_kv *kv) { return kv ? kv->last_grid : 0; }
+
+long long wick_hip_kv_scratch_bytes(const wick_hip_kv *kv) {
+    if (!kv) return 0;
+    size_t floats = kv->q_cap + kv->att_cap + 2 * kv->kst_cap + kv->io_cap + kv->io_host_cap;
+    if (kv->part) floats += wick::decode_workspace_floats(kv->ws_units, kv->head_dim);
+    return (long long)(floats * sizeof(float));
+}
 
 int wick_hip_kv_append_device(wick_hip_kv *kv, int layer, int start, int t, const float *k_dev, const float *v_dev) {
     int rc = check_kv(kv, layer);

@@ -1196,56 +1196,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
 // ------------------------------------------------------------------ prefill
 
 // Rows of one kv head are the flattened (token i, head hh) pairs r = i*group + hh,
-// so the GQA heads of a token share every K/V tile.  Each wave owns a block of
-// 16 rows and runs over all keys that block can see (0 .. start + last token),
-// masking per row; with pairing, a wave takes row blocks b and nblocks-1-b so
-// that every wave of a causal launch does the same amount of work.
-template <int D>
-__device__ __forceinline__ void prefill_block(const PrefillArgs &a, const float *Kh, const float *Vh, int kvh, int b,
-                                              int lane) {
-    using S = Shape<D>;
-    const int col = lane & 15, g = lane >> 4;
-    const int heads = a.kv_heads * a.group;
-    const int nrows = a.t * a.group;
-    const int r = 16 * b + col;
-    const bool valid = r < nrows;
-    const int i = valid ? r / a.group : 0, hh = valid ? r % a.group : 0;
-    const int lim = valid ? a.start + i + 1 : 1;
-    const int imax = min(16 * b + 15, nrows - 1) / a.group;
-    const int kend = a.start + imax + 1;
-    const size_t qoff = (size_t)i * heads * D + (size_t)(kvh * a.group + hh) * D;
-
-    f4 q[S::KJ];
-    load_q<D>(a.q + qoff, a.q, valid, lane, q);
-    WaveState<D> st;
-    init_state<D>(st);
-    attend_range<D>(Kh, Vh, 0, kend, 0, S::TG, lim, a.scale, q, lane, st);
-    const float inv_l = 1.0f / col_sum(st.l);
-    if (!valid) return;
-    float *out = a.att + qoff;
-#pragma unroll
-    for (int db = 0; db < S::DB; db++)
-#pragma unroll
-        for (int rr = 0; rr < 4; rr++) out[out_dim<D>(g, rr, db)] = st.o[db][rr] * inv_l;
-}
-
-template <int D>
-__global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int kvh = blockIdx.x % a.kv_heads;
-    const int item = (blockIdx.x / a.kv_heads) * 4 + w;
-    if (item >= a.items) return;
-    const float *Kh = a.k + (size_t)kvh * a.capacity * D;
-    const float *Vh = a.v + (size_t)kvh * a.capacity * D;
-    if (a.paired) {
-        const int b1 = a.nblocks - 1 - item;
-        prefill_block<D>(a, Kh, Vh, kvh, b1, lane);
-        if (b1 != item) prefill_block<D>(a, Kh, Vh, kvh, item, lane);
-    } else {
-        prefill_block<D>(a, Kh, Vh, kvh, item, lane);
-    }
-}
-
+// so the GQA heads of a token share every K/V tile.
 // Workgroup = one 16-row block b of one kv head; its causal key range
 // 0 .. start + last token of the block is split into 4 contiguous tile ranges,
 // one per wave, whose states are merged through LDS.  Blocks are dispatched
@@ -1659,17 +1610,17 @@ hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_
     return hipGetLastError();
 }
 
-bool decode_oproj_supported(int head_dim, int group, int nchunks) {
-    if (nchunks != 1 || (head_dim != 64 && head_dim != 128)) return false;
+bool decode_oproj_supported(int head_dim, int group, int nchunks, int chunk) {
+    // one chunk per unit, of at most kOprojMaxChunk keys: each wave of a
+    // workgroup takes at most one group of tiles (8 waves x 32 keys at head_dim
+    // 64; head_dim 128 loops over 16-key groups)
+    if (nchunks != 1 || chunk > kOprojMaxChunk || (head_dim != 64 && head_dim != 128)) return false;
     const int ncols = group < kTileRows ? group : kTileRows;
     return ncols * head_dim <= 64 * kOprojChunks;
 }
 
 hipError_t launch_decode_oproj(int head_dim, DecodeArgs a, hipStream_t s) {
-    // each wave of a workgroup takes at most one group of tiles (chunk <= 8
-    // waves x 32 keys at head_dim 64; head_dim 128 loops over 16-key groups)
-    if (!a.prep || !decode_oproj_supported(head_dim, a.group, a.nchunks) || a.chunk > 8 * 2 * 16)
-        return hipErrorInvalidValue;
+    if (!a.prep || !decode_oproj_supported(head_dim, a.group, a.nchunks, a.chunk)) return hipErrorInvalidValue;
     // 8 waves split the keys, one wo row each: the widest grid measured best
     // (1, 2, 4 rows per wave: 216 / 108 / 54 workgroups for SmolLM2, e2e
     // 1845 / 1824 / 1795 tok/s; 4 waves per workgroup 1728)
@@ -1702,8 +1653,7 @@ int prefill_blocks_per_cu(int head_dim, int rows32) {
     return (e == hipSuccess && n > 0) ? n : 1;
 }
 
-bool prefill_has_rows32(int head_dim, int capacity, int split) {
-    if (!split) return false;
+bool prefill_has_rows32(int head_dim, int capacity) {
     if (head_dim == 128) return capacity <= lean_max_capacity<128>();
     if (head_dim == 64) return capacity <= lean_max_capacity<64>();
     return false;
@@ -1711,12 +1661,12 @@ bool prefill_has_rows32(int head_dim, int capacity, int split) {
 
 // A lean kernel with two row blocks per workgroup.
 static bool prefill_uses_rows32(int head_dim, const PrefillArgs &a) {
-    return a.rows32 && prefill_has_rows32(head_dim, a.capacity, a.split);
+    return a.rows32 && prefill_has_rows32(head_dim, a.capacity);
 }
 
 int prefill_grid(int head_dim, const PrefillArgs &a) {
     if (prefill_uses_rows32(head_dim, a)) return a.kv_heads * ((a.nblocks + 1) / 2);
-    return a.split ? a.kv_heads * a.nblocks : a.kv_heads * ((a.items + 3) / 4);
+    return a.kv_heads * a.nblocks;
 }
 
 hipError_t launch_prefill(int head_dim, const PrefillArgs &a, hipStream_t s) {
@@ -1725,16 +1675,14 @@ hipError_t launch_prefill(int head_dim, const PrefillArgs &a, hipStream_t s) {
         hipLaunchKernelGGL(prefill_lean2_kernel_d128, dim3(grid), dim3(256), 0, s, a);
     } else if (prefill_uses_rows32(head_dim, a)) {
         hipLaunchKernelGGL(prefill_lean2_kernel_d64, dim3(grid), dim3(256), 0, s, a);
-    } else if (a.split && head_dim == 128 && a.capacity <= lean_max_capacity<128>()) {
+    } else if (head_dim == 128 && a.capacity <= lean_max_capacity<128>()) {
         hipLaunchKernelGGL(prefill_lean_kernel_d128, dim3(grid), dim3(256), 0, s, a);
-    } else if (a.split && head_dim == 64 && a.capacity <= lean_max_capacity<64>()) {
+    } else if (head_dim == 64 && a.capacity <= lean_max_capacity<64>()) {
         hipLaunchKernelGGL(prefill_lean_kernel_d64, dim3(grid), dim3(256), 0, s, a);
-    } else if (a.split && head_dim == 128) {
+    } else if (head_dim == 128) {
         hipLaunchKernelGGL(prefill_split_kernel_d128, dim3(grid), dim3(256), 0, s, a);
-    } else if (a.split) {
-        WICK_DISPATCH_D(head_dim, prefill_split_kernel, dim3(grid), dim3(256), 0, s, a);
     } else {
-        WICK_DISPATCH_D(head_dim, prefill_kernel, dim3(grid), dim3(256), 0, s, a);
+        WICK_DISPATCH_D(head_dim, prefill_split_kernel, dim3(grid), dim3(256), 0, s, a);
     }
     return hipGetLastError();
 }

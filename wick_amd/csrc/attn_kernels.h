@@ -54,15 +54,16 @@ struct DecodeArgs {
 // unit's output (ncols * head_dim <= 64 * kOprojChunks).
 constexpr int kOprojRows = 1;
 constexpr int kOprojChunks = 4;
+// Longest chunk the fused form takes (8 waves x one 32-key group each).
+constexpr int kOprojMaxChunk = 8 * 2 * 16;
 
 struct PrefillArgs {
     const float *q;   // [t][heads*D]
     const float *k;   // layer base, [kv_heads][capacity][D]
     const float *v;
     float *att;       // [t][heads*D]
-    int capacity, t, start, kv_heads, group, nblocks, items, paired;
-    int split;        // 1: prefill_split_kernel (4-way key split per workgroup)
-    int zigzag;       // split kernel: the grid is resident at once; pair heavy and light blocks
+    int capacity, t, start, kv_heads, group, nblocks;
+    int zigzag;       // the grid is resident at once; pair heavy and light blocks
     int rows32;       // lean kernels: two 16-row blocks per workgroup
     float scale;
 };
@@ -101,13 +102,14 @@ int decode_blocks_per_cu(int head_dim);
 // The same for the split prefill kernel.
 int prefill_blocks_per_cu(int head_dim, int rows32);
 // Whether the prefill kernel for this shape can take two row blocks per workgroup.
-bool prefill_has_rows32(int head_dim, int capacity, int split);
+bool prefill_has_rows32(int head_dim, int capacity);
 
 // Launches decode_kernel and, when it splits the keys, decode_merge_kernel.
 hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_t s);
-// Whether decode_kernel's fused output projection serves this shape (head_dim
-// 64 or 128, one chunk per unit, the unit's columns fit kOprojChunks).
-bool decode_oproj_supported(int head_dim, int group, int nchunks);
+// Whether decode_kernel's fused output projection serves this plan (head_dim
+// 64 or 128, one chunk of at most kOprojMaxChunk keys per unit, the unit's
+// columns fit kOprojChunks).
+bool decode_oproj_supported(int head_dim, int group, int nchunks, int chunk);
 // The fused decode + partial output projection (a.prep set, a.nchunks == 1):
 // units x ceil(hidden / (8 kOprojRows)) workgroups of 8 waves.
 hipError_t launch_decode_oproj(int head_dim, DecodeArgs a, hipStream_t s);

@@ -138,3 +138,7 @@ class DeviceKvCache:
 
     def last_grid(self):
         return self._lib.wick_hip_kv_last_grid(self.handle)
+
+    def scratch_bytes(self):
+        """Staging and decode workspace bytes the handle has allocated so far."""
+        return int(self._lib.wick_hip_kv_scratch_bytes(self.handle))

@@ -8,9 +8,14 @@ a caller-supplied generator (bench.py passes wick's, see `normal` below); norm
 weights are 1.0 (the Hugging Face initialisation).  wick_prompt() draws token
 ids with wick's own generator.
 """
+import ctypes
+import os
+
 import numpy as np
 
 from .model import Config
+
+PROBE_LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libwick_probe.so")
 
 _M64 = (1 << 64) - 1
 
@@ -80,3 +85,35 @@ def random_weights(cfg, seed=0, std=0.02, normal=None):
 
 def random_prompt(seed, n, vocab):
     return np.random.default_rng(seed).integers(0, vocab, n).astype(np.uint32)
+
+
+class DeviceNormals:
+    """A configuration's N(0, 1) inputs from wick's generator, made on the GPU:
+    xoshiro256** seeded through splitmix64 with the configuration's seed
+    (/root/reference/src/sampler.rs:28-55), Box-Muller in double, times a scale,
+    by libwick_probe.so's wick_synth_normal.  The i-th tensor asked for reads
+    substream i of the seed's stream (i long jumps), its rows successive jumps,
+    so any tensor's rows are known without drawing the ones before them."""
+
+    def __init__(self, torch, device, seed):
+        self.torch, self.device, self.seed, self.count = torch, device, seed, 0
+        self.lib = ctypes.CDLL(PROBE_LIB)
+        self.lib.wick_synth_normal.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_int,
+                                               ctypes.c_ulonglong, ctypes.c_float, ctypes.c_void_p]
+
+    def normal(self, rows, cols, scale=1.0):
+        """The next tensor, [rows][cols] f32 on the device (synchronous on torch's current stream)."""
+        x = self.torch.empty(rows, cols, device=self.device)
+        rc = self.lib.wick_synth_normal(x.data_ptr(), self.count, rows, cols, self.seed, scale,
+                                        self.torch.cuda.current_stream().cuda_stream)
+        if rc:
+            raise RuntimeError(f"wick_synth_normal: HIP error {rc}")
+        self.count += 1
+        return x
+
+
+def wick_generator_weights(torch, cfg, seed=0, std=0.02, device="cuda"):
+    """random_weights(cfg) with every matrix drawn by wick's generator (seed `seed`,
+    N(0, std)) on the GPU and copied to host memory: the e2e configuration's weights."""
+    syn = DeviceNormals(torch, device, seed)
+    return random_weights(cfg, normal=lambda rows, cols, s: syn.normal(rows, cols, s).cpu().numpy())
