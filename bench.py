@@ -439,6 +439,7 @@ def measure_long_decode(torch, kv_cls, native, dev, steps, ceiling=True, check_t
                       "us_per_layer": round(ms_launch * 1e3, 2), "GBps": round(gbs, 1),
                       "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 1)})
     kv.set_option(native.OPT_DECODE_CHUNK, 0)
+    progress("long decode: chunk sweep timed")
 
     # The same shape at a 32K context (the first 32768 positions of each layer,
     # 268 MB per layer): the headline's context length with a larger per-layer
@@ -833,6 +834,7 @@ def main():
             # every launch of the step wrote the same outputs; keep this length's
             torch.cuda.synchronize()
             decode_outs[L] = att.cpu().numpy()
+    progress("decode lengths timed")
     # HBM bytes per launch measured by the committed rocprofv3 --pmc runs on this
     # same workload (FETCH_SIZE / WRITE_SIZE scaled by a copy of known size).
     # They hold for the kernel source they were measured on: the summary records
@@ -842,6 +844,7 @@ def main():
     if not args.no_ceiling:
         ceiling = measure_ceiling(torch, stream, dev, 2 * c["L"] * c["kv_heads"] * c["d"] * 4, c["layers"],
                                   args.steps, args.warmup)
+    progress("read ceiling measured")
     bytes_layer = decode_bytes(c["L"], c["heads"], c["kv_heads"], c["d"])
     bytes_step = bytes_layer * c["layers"]
     value = bytes_step / (ms_step * 1e-3) / 1e9
