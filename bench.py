@@ -16,11 +16,18 @@ value  = algorithmic bytes per step / step time, in GB/s, where one layer
          both ways (the faster kept).
 Also reported: causal prefill TFLOP/s (Qwen3 shape, T = 512 and 2048), chunked
 prefill (TinyLlama shape, 512 tokens onto 1536 cached), long-context decode with
-a split-K chunk sweep (Llama-3-8B shape, 65536 positions), e2e decode tok/s
-(SmolLM2-135M architecture, wick's cmd_bench loop) and the CPU oracle timed on
-the host cores on a bounded sample (cpu_baseline).
+a split-K chunk sweep (Llama-3-8B shape, 65536 positions, and the same shape at
+32768 with its own read ceiling), e2e decode tok/s (SmolLM2-135M architecture,
+wick's cmd_bench loop) and the CPU oracle timed on the host cores on a bounded
+sample (cpu_baseline).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+parity: after each configuration's timing, outside every timed region, its GPU
+outputs on the bench's own inputs are compared with the CPU oracle (wick's
+attention restated in C): max abs / max rel error and whether every element is
+within 2e-5 + 1e-4 |ref|; for configs[0] the oracle's 65 greedy ids against both
+GPU paths and every layer's attention, teacher-forced.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-parity] [--no-cpu]
 """
 import argparse
 import json
