@@ -409,6 +409,24 @@ def measure_prefill(torch, kv_cls, dev, heads, kv_heads, d, T, start, theta, see
     return ms * 1e3, prefill_flops(T, heads, d, start), rec
 
 
+def long_decode_layer_inputs(torch, dev, layer=0):
+    """configs[4]'s inputs for one layer exactly as measure_long_decode draws them:
+    the layer's K rows (RoPE'd at positions 0..L-1) and V rows -- the seed's tensors
+    2*layer and 2*layer+1 -- and the layer's q row (row `layer` of tensor 2*layers,
+    RoPE'd at L-1).  Device tensors [L][Hkv*d], [L][Hkv*d], [1][Hq*d]."""
+    c = LONG
+    g = DeviceNormals(torch, dev, c["seed"])
+    inv = inv_freq_torch(c["theta"], c["d"], dev)
+    g.count = 2 * layer
+    k = rope_torch(g.normal(c["L"], c["kv_heads"] * c["d"]), c["kv_heads"], c["d"],
+                   torch.arange(c["L"], device=dev), inv).contiguous()
+    v = g.normal(c["L"], c["kv_heads"] * c["d"])
+    g.count = 2 * c["layers"]
+    q = rope_torch(g.normal(c["layers"], c["heads"] * c["d"]), c["heads"], c["d"],
+                   torch.full((c["layers"],), c["L"] - 1, device=dev), inv)[layer:layer + 1].contiguous()
+    return k, v, q
+
+
 def measure_long_decode(torch, kv_cls, native, dev, steps, ceiling=True, check_threads=0):
     """32 layers x 65536 positions (16 GiB of K+V), one token per layer per step.
     check_threads > 0: layer 0's outputs at 65536 and 32768 positions are checked
