@@ -4,9 +4,10 @@ smollm2_135m() is the SmolLM2-135M architecture of the e2e benchmark: Llama, 30 
 hidden 576, 9 query / 3 KV heads, head_dim 64, FFN 1536 SiLU-gated, RMSNorm eps
 1e-5, RoPE theta 10000, vocab 49152, tied embeddings.  Matrices are f32
 N(0, std) in a fixed order -- drawn with numpy's PCG64 from the given seed, or by
-a caller-supplied generator (bench.py passes wick's, see `normal` below); norm
-weights are 1.0 (the Hugging Face initialisation).  wick_prompt() draws token
-ids with wick's own generator.
+a caller-supplied generator (`normal` below); norm weights are 1.0 (the Hugging
+Face initialisation).  wick_generator_weights() draws them with wick's own
+generator on the device (DeviceNormals, the benchmark's inputs), and
+wick_prompt() draws token ids with it on the host.
 """
 import ctypes
 import os
