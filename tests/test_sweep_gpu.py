@@ -3,7 +3,7 @@ against the CPU oracle.
 
 Each case draws a head_dim, kv heads, GQA group, cache length and chunk length
 (decode t = 1, short chunks, long chunks), and sometimes a forced decode chunk
-size, so the cases fall on the one-chunk and split decode paths (MFMA and VALU
+size (16-key steps, not always whole tile groups), so the cases fall on the one-chunk and split decode paths (MFMA and VALU
 cores, 4- and 8-wave workgroups, every merge slot count), the prefill kernels
 and the preparation paths (bias, QK-norm, RoPE) without naming them.  Outputs
 within 2e-5 abs / 1e-4 rel of the oracle; appended cache rows bit-exact.
@@ -32,7 +32,7 @@ def draw(rng):
     else:
         t = int(rng.integers(40, 300))
     start = int(rng.integers(0, 6000 if t == 1 else 1500))
-    chunk = int(rng.choice([0, 0, 0, 64, 128, 512])) if t == 1 else 0
+    chunk = int(rng.choice([0, 0, 0, 64, 80, 128, 208, 336, 512])) if t == 1 else 0
     return d, kv_heads, group, t, start, chunk
 
 
