@@ -139,6 +139,7 @@ int wick_hip_kv_synchronize(wick_hip_kv *kv);
 
 /* Tuning knobs. */
 #define WICK_HIP_OPT_DECODE_CHUNK 1 /* positions per decode workgroup (a multiple of 16, at least 64; 0 = automatic) */
+#define WICK_HIP_OPT_DECODE_ORDER 2 /* split-K key order: 1 = automatic (interleaved on long contexts; default), 0 = contiguous chunks */
 int wick_hip_kv_set_option(wick_hip_kv *kv, int option, int value);
 
 /* Number of workgroups the last attention call launched (for measurement). */

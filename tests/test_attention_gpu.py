@@ -98,6 +98,49 @@ def test_decode_chunk_option_values():
                 kv.set_option(_native.OPT_DECODE_CHUNK, bad)
         for good in (0, 64, 80, 4096):
             kv.set_option(_native.OPT_DECODE_CHUNK, good)
+        for bad in (-1, 2, 3):
+            with pytest.raises(_native.WickHipError):
+                kv.set_option(_native.OPT_DECODE_ORDER, bad)
+        for good in (0, 1):
+            kv.set_option(_native.OPT_DECODE_ORDER, good)
+
+
+# The interleaved split order applies when the kv head's key groups (16 keys at
+# head_dim 128, 32 at 64) give each of the nchunks x 4 waves at least 4 full rounds.
+def interleaved(L, d, nchunks):
+    gk = 16 if d == 128 else 32
+    return (L + gk - 1) // gk >= 4 * nchunks * 4
+
+
+@pytest.mark.parametrize("d,heads,kv_heads,chunk,L", [
+    (128, 32, 8, 512, 5000),     # 10 chunks, 313 groups: 7 full rounds + a partial one
+    (128, 32, 8, 256, 4096),     # 16 chunks, 256 groups: exactly 4 full rounds, no partial one
+    (128, 8, 2, 1024, 9001),     # ragged last group
+    (64, 14, 2, 1024, 6000),     # double-buffered core, 32-key groups
+    (64, 40, 2, 1024, 4500),     # two 16-head slices per kv head (4 units); a partial round of one group
+])
+def test_decode_key_orders(d, heads, kv_heads, chunk, L):
+    """Both split-K key orders against the oracle, on plans where the automatic
+    order interleaves key groups across a kv head's workgroups (every unit
+    starting its rounds at a different one), and bit-stable from call to call."""
+    nchunks = -(-L // chunk)
+    assert interleaved(L, d, nchunks)
+    q, k, v = make_inputs(L + d, 1, L - 1, heads, kv_heads, d)
+    want = ol.attention(q, k, v, 1, L - 1, heads, kv_heads, d)
+    outs = {}
+    with DeviceKvCache(1, L, kv_heads, d) as kv:
+        kv.append(0, 0, k, v)
+        kv.set_option(_native.OPT_DECODE_CHUNK, chunk)
+        for order in (0, 1):
+            kv.set_option(_native.OPT_DECODE_ORDER, order)
+            outs[order] = kv.attention(0, heads, q, L - 1)
+            again = kv.attention(0, heads, q, L - 1)
+            assert np.array_equal(outs[order].view(np.uint32), again.view(np.uint32)), "not bit-stable"
+            ok, mabs, mrel = within_tol(outs[order], want)
+            print(f"order {order}: {kv.last_grid()} workgroups, max abs {mabs:.2e} max rel {mrel:.2e}")
+            assert ok, (order, mabs, mrel)
+    # a different summation order: equal within rounding, not bit-identical
+    assert np.abs(outs[0] - outs[1]).max() < 1e-5
 
 
 def test_long_decode_steps_append_llama3_8b_shape():

@@ -85,6 +85,49 @@ def test_decode_prep_with_split_chunks():
     run_chunks(14, 2, 64, [700, 1, 1], 1e6, bias=True, norm=True)
 
 
+@pytest.mark.parametrize("heads,kv_heads,d,chunk,base", [(32, 8, 128, 512, 1918), (14, 2, 64, 1024, 2900)])
+def test_decode_prep_interleaved_new_key_not_in_last_chunk(heads, kv_heads, d, chunk, base):
+    """Single-token steps with the preparation in the decode kernel's prologue,
+    on plans that interleave key groups across a kv head's workgroups: the new
+    position's k and v rows are prepared and appended by the workgroups whose
+    groups hold it, which here are not the last chunk's."""
+    gk = 16 if d == 128 else 32
+    inv = ol.rope_inv_freq(1e6, d)
+    rng = np.random.default_rng(base)
+    steps, eps = 4, 1e-6
+    cap = base + steps
+    cpu_k = np.zeros((cap, kv_heads * d), np.float32)
+    cpu_v = np.zeros((cap, kv_heads * d), np.float32)
+    cpu_k[:base] = rng.standard_normal((base, kv_heads * d), dtype=np.float32)
+    cpu_v[:base] = rng.standard_normal((base, kv_heads * d), dtype=np.float32)
+    n = (rng.uniform(0.5, 1.5, d).astype(np.float32), rng.uniform(0.5, 1.5, d).astype(np.float32))
+    not_last = []
+    with DeviceKvCache(1, cap, kv_heads, d) as kv:
+        kv.set_rope(inv)
+        kv.set_option(_native.OPT_DECODE_CHUNK, chunk)
+        kv.set_prep(0, heads, q_norm=n[0], k_norm=n[1], eps=eps)
+        kv.append(0, 0, cpu_k[:base], cpu_v[:base])
+        for s in range(steps):
+            start = base + s
+            L = start + 1
+            nchunks = -(-L // chunk)
+            assert -(-L // gk) >= 4 * nchunks * 4, "plan does not interleave"
+            not_last.append((L - 1) // (4 * gk) % nchunks != nchunks - 1)
+            q, k, v, _, _ = raw_inputs(base + 100 + s, 1, heads, kv_heads, d)
+            att = kv.attend(0, heads, q, k, v, start)
+            pq, pk, pv = ol.prep(q, k, v, heads, kv_heads, d, start, inv, norms=n, eps=eps)
+            cpu_k[start] = pk[0]
+            cpu_v[start] = pv[0]
+            gk_rows, gv_rows = kv.read(0, 0, L)
+            assert np.array_equal(gk_rows.view(np.uint32), cpu_k[:L].view(np.uint32)), "K cache not bit-exact"
+            assert np.array_equal(gv_rows.view(np.uint32), cpu_v[:L].view(np.uint32)), "V cache not bit-exact"
+            want = ol.attention(pq, cpu_k[:L], cpu_v[:L], 1, start, heads, kv_heads, d)
+            ok, mabs, mrel = within_tol(att, want)
+            print(f"step {s}: L={L} {kv.last_grid()} workgroups, max abs {mabs:.2e} rel {mrel:.2e}")
+            assert ok, (s, mabs, mrel)
+    assert all(not_last)
+
+
 def test_decode_prep_with_head_slices():
     # group 20 > 16: two head slices per kv head both prepare (identical) k and v
     run_chunks(40, 2, 64, [50, 1, 1], 1e4, bias=True, norm=True)

@@ -17,6 +17,7 @@ ENOMEM = -3
 EDEVICE = -4
 
 OPT_DECODE_CHUNK = 1
+OPT_DECODE_ORDER = 2
 
 # Every symbol include/*.h declares, with its ctypes signature.
 _P = ctypes.c_void_p

@@ -65,7 +65,7 @@ struct wick_hip_kv {
     // whether the static workspace's address was found on this device
     hipError_t static_rc = hipErrorNotInitialized;
     // options
-    int decode_chunk = 0, last_grid = 0;
+    int decode_chunk = 0, decode_interleave = 1, last_grid = 0;
     int decode_blocks_per_cu = 1, prefill_blocks_per_cu = 1, prefill2_blocks_per_cu = 1;
     // input preparation (wick_hip_kv_set_rope / wick_hip_kv_set_prep)
     float *rope_cos = nullptr, *rope_sin = nullptr;  // [capacity][head_dim/2]
@@ -215,6 +215,7 @@ int plan_decode(wick_hip_kv *kv, int layer, int group, int len, const float *q_d
     a->chunk = chunk;
     a->nchunks = nchunks;
     a->stagger = nchunks > 1 && (long long)units * nchunks >= 2LL * kv->num_cus ? 1 : 0;
+    a->interleave = kv->decode_interleave;
     kv->last_grid = units * nchunks;
     return WICK_HIP_OK;
 }
@@ -526,6 +527,12 @@ int wick_hip_kv_set_option(wick_hip_kv *kv, int option, int value) {
         if (value != 0 && (value < 64 || value % 16 != 0))
             return fail(WICK_HIP_EINVAL, "decode chunk must be 0 or a multiple of 16 of at least 64 (got %d)", value);
         kv->decode_chunk = value;
+        return WICK_HIP_OK;
+    case WICK_HIP_OPT_DECODE_ORDER:
+        if (value != 0 && value != 1)
+            return fail(WICK_HIP_EINVAL, "decode order must be 0 (contiguous chunks) or 1 (automatic) (got %d)",
+                        value);
+        kv->decode_interleave = value;
         return WICK_HIP_OK;
     default:
         return fail(WICK_HIP_EINVAL, "unknown option %d", option);

@@ -781,6 +781,52 @@ __device__ __forceinline__ void valu_core(const float *__restrict__ Kh, const fl
 
 // ------------------------------------------------------------------ decode
 
+// The key groups one wave of a split decode takes, in order: n groups of gk
+// keys, the first at position p; next(p, j) gives the position of group j + 1
+// from group j's.  All fields are wave-uniform.
+//   contiguous: positions p, p + step, ... below the chunk's end.
+//   interleaved: the kv head's groups dealt round-robin to the waves of its
+//     nchunks workgroups (slot = chunk * waves + wave): F full rounds of
+//     `slots` groups, then one partial round.  Unit u starts its full rounds
+//     at round u mod F, so the kv heads (each on its own XCD when there are
+//     8 units) do not read the same offsets of their caches at the same time
+//     (without the rotation the Llama-3-8B shape at 32768 positions ran
+//     48.6-48.8 us against 46.7-46.8).
+struct KeyWalk {
+    int p, n, step, wrap, full, tailp;
+
+    __device__ static KeyWalk contiguous(int p0, int end, int step) {
+        KeyWalk k;
+        k.p = __builtin_amdgcn_readfirstlane(p0);
+        k.n = __builtin_amdgcn_readfirstlane(p0 < end ? (end - p0 + step - 1) / step : 0);
+        k.step = step;
+        k.wrap = 0x7fffffff;
+        k.full = -1;
+        k.tailp = 0;
+        return k;
+    }
+
+    __device__ static KeyWalk interleaved(int len, int nchunks, int chunk, int waves, int w, int gk, int unit) {
+        const int slots = nchunks * waves, ngroups = (len + gk - 1) / gk;
+        const int F = ngroups / slots, base = (chunk * waves + w) * gk, span = F * slots * gk;
+        const int rot = F > 0 ? unit % F : 0;
+        KeyWalk k;
+        k.n = __builtin_amdgcn_readfirstlane(F + (span + base < len ? 1 : 0));
+        k.p = __builtin_amdgcn_readfirstlane(rot * slots * gk + base);
+        k.step = slots * gk;
+        k.wrap = span;
+        k.full = F;
+        k.tailp = __builtin_amdgcn_readfirstlane(span + base);
+        return k;
+    }
+
+    __device__ int next(int pos, int j) const {
+        if (j + 1 == full) return tailp;
+        pos += step;
+        return pos >= wrap ? pos - wrap : pos;
+    }
+};
+
 // Partial states of the split-K decode, per (unit, column): O [units][16][256][D],
 // m and l [units][16][256] (unit = kv head x 16-head slice, column = query head
 // of the slice, 256 = most chunks per call).  The chunk states of a column are
@@ -851,7 +897,19 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
     const float *Vh = a.v + (size_t)kvh * a.capacity * D;
     // the cache length: the argument, or (graph-replayed decode loop) a device counter
     const int len = a.len_dev ? *a.len_dev : a.len;
-    const int kbeg = chunk * a.chunk, kend = min(kbeg + a.chunk, len);
+    // Interleaved split (DecodeArgs::interleave; KeyWalk): at any moment the
+    // workgroups of a kv head read one window of its cache rather than
+    // nchunks streams a chunk apart.  It pays from kDecodeInterleaveRounds
+    // full rounds of groups per wave (Llama-3-8B shape: 65536 positions
+    // 84.8 -> 83.2 us, 32768 47.6 -> 46.7 us) and loses below (16384: 27.4
+    // -> 28.3-29.3 us, 8192: 17.1 -> 17.5 us).  owner: the chunk that holds
+    // position len-1.
+    constexpr int GKc = 16 * TG;
+    const bool ilv = NC == 0 && D >= 64 && !OPROJ && a.interleave && a.nchunks > 1 &&
+                     (len + GKc - 1) / GKc >= kDecodeInterleaveRounds * a.nchunks * NW;
+    const int kbeg = ilv ? chunk * NW * GKc : chunk * a.chunk;
+    const int kend = ilv ? len : min(kbeg + a.chunk, len);
+    const int owner = ilv ? (len - 1) / (NW * GKc) % a.nchunks : a.nchunks - 1;
 
     // OPROJ: this wave's kOprojRows rows of wo over the unit's ncols*D
     // columns, requested before anything waits on memory: lane l holds column
@@ -877,12 +935,12 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
     float qkeep;  // 0 for the padding columns past the unit's ncols heads
     if constexpr (PREP && !RP) {
         // Rows: the unit's ncols q heads (to LDS), then -- in the workgroups
-        // of the last chunk, the only ones that read position len-1 -- the new
-        // k and v rows of the kv head (to the cache).  Workgroups of other
+        // of the chunk that holds position len-1, the only ones that read it
+        // -- the new k and v rows of the kv head (to the cache).  Workgroups of other
         // head slices of the same kv head write the same bits there.  The
         // barrier orders those stores before this workgroup's tile loads.
         const int pos = len - 1;
-        const bool last = chunk == a.nchunks - 1;
+        const bool last = chunk == owner;
         const int nrows = ncols + (last ? 2 : 0);
         const float *cr = a.rope_cos + (size_t)pos * (D / 2), *sr = a.rope_sin + (size_t)pos * (D / 2);
         float *Kw = a.k + ((size_t)kvh * a.capacity + pos) * D;
@@ -924,8 +982,8 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
             rp.kc = a.k + ((size_t)kvh * a.capacity + pos) * D;
             rp.vc = a.v + ((size_t)kvh * a.capacity + pos) * D;
             rp.eps = a.eps;
-            // only the last chunk holds position len - 1
-            rp.newkey = chunk == a.nchunks - 1 ? pos : -1;
+            // only the owner chunk holds position len - 1 (the last one here)
+            rp.newkey = chunk == owner ? pos : -1;
             valu_core<NC, NW, true>(Kh, Vh, qr, a.scale * kLog2e, kbeg, kend, w, lane, swts, sm_m, sm_l, sm_o, rp,
                                     sqw[w]);
         } else {
@@ -960,27 +1018,29 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
         for (int db = 0; db < S::DB; db++) st.o[db] = f4{0.f, 0.f, 0.f, 0.f};
         constexpr int GK = 16 * TG;                 // keys per group
         constexpr bool kStreamV = D == 128 || PP;  // V through the streaming policy (lean_load_global_v)
-        const int wbeg = __builtin_amdgcn_readfirstlane(kbeg + GK * w), step = NW * GK;
+        const KeyWalk walk = ilv ? KeyWalk::interleaved(len, a.nchunks, chunk, NW, w, GK, unit)
+                                 : KeyWalk::contiguous(kbeg + GK * w, kend, NW * GK);
+        const int n = walk.n;
         if constexpr (PP) {
             // the next group's loads go out before this group's products
             LeanGroup<D, TG> ta, tb;
-            int p0 = wbeg;
-            if (p0 < kend) lean_load_global<D, TG, kStreamV>(Kh, Vh, p0, kend, p0 + GK > kend, lane, ta);
+            int p0 = walk.p;
+            if (n > 0) lean_load_global<D, TG, kStreamV>(Kh, Vh, p0, kend, p0 + GK > kend, lane, ta);
             __builtin_amdgcn_sched_barrier(0);
             scale_q();
-            while (p0 < kend) {
-                const int p1 = p0 + step;
-                if (p1 < kend) lean_load_global<D, TG, kStreamV>(Kh, Vh, p1, kend, p1 + GK > kend, lane, tb);
+            for (int j = 0; j < n; j += 2) {
+                const int p1 = walk.next(p0, j);
+                if (j + 1 < n) lean_load_global<D, TG, kStreamV>(Kh, Vh, p1, kend, p1 + GK > kend, lane, tb);
                 lean_step<D, false, TG>(ta, q, p0, p0 + GK > kend, kend, g, st.m, st.l, st.o);
-                if (p1 >= kend) break;
-                const int p2 = p1 + step;
-                if (p2 < kend) lean_load_global<D, TG, kStreamV>(Kh, Vh, p2, kend, p2 + GK > kend, lane, ta);
+                if (j + 1 >= n) break;
+                const int p2 = walk.next(p1, j + 1);
+                if (j + 2 < n) lean_load_global<D, TG, kStreamV>(Kh, Vh, p2, kend, p2 + GK > kend, lane, ta);
                 lean_step<D, false, TG>(tb, q, p1, p1 + GK > kend, kend, g, st.m, st.l, st.o);
                 p0 = p2;
             }
         } else {
-            int p0 = wbeg;
-            if (p0 < kend) {
+            int p0 = walk.p, j = 0;
+            if (n > 0) {
                 LeanGroup<D, TG> t;
                 const bool tail = p0 + GK > kend;
                 lean_load_global_k<D, TG>(Kh, p0, kend, tail, lane, t);
@@ -994,9 +1054,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
                 if (a.stagger) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 lean_load_global_v<D, TG, kStreamV>(Vh, p0, kend, tail, lane, t);
                 lean_step<D, false, TG>(t, q, p0, tail, kend, g, st.m, st.l, st.o);
-                p0 += step;
+                p0 = walk.next(p0, j++);
             }
-            for (; p0 < kend; p0 += step) {
+            for (; j < n; p0 = walk.next(p0, j++)) {
                 LeanGroup<D, TG> t;
                 const bool tail = p0 + GK > kend;
                 lean_load_global<D, TG, kStreamV>(Kh, Vh, p0, kend, tail, lane, t);

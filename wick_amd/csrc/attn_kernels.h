@@ -27,10 +27,17 @@ struct DecodeArgs {
     // a grid of at least two workgroups per CU, streaming from HBM: each wave
     // requests its first group's V rows only once its K rows have arrived
     int stagger;
+    // Key order of a split (several chunks, head_dim 64 / 128 on the MFMA
+    // tiles): 0 = chunk c takes positions c*chunk .. +chunk; 1 = interleaved
+    // where the length the kernel reads gives every wave at least
+    // kDecodeInterleaveRounds full rounds: wave w of chunk c takes the key
+    // groups (i*nchunks + c)*waves + w of the whole context (rounds i rotated
+    // per unit), contiguous chunks otherwise.
+    int interleave;
     float scale;
     // Fused input preparation (prep != 0): q is raw; kraw / vraw [kv_heads*D]
     // are the new token's raw k and v, prepared and appended at position len-1
-    // by the workgroups that own the last chunk.  Biases / norms may be null.
+    // by the workgroups of the chunk that holds it.  Biases / norms may be null.
     int prep;
     const float *kraw, *vraw;
     const float *bq, *bk, *bv, *qn, *kn;
@@ -56,6 +63,9 @@ constexpr int kOprojRows = 1;
 constexpr int kOprojChunks = 4;
 // Longest chunk the fused form takes (8 waves x one 32-key group each).
 constexpr int kOprojMaxChunk = 8 * 2 * 16;
+
+// Fewest full rounds of key groups per wave for the interleaved split order.
+constexpr int kDecodeInterleaveRounds = 4;
 
 struct PrefillArgs {
     const float *q;   // [t][heads*D]
