@@ -963,23 +963,23 @@ def main():
     if check:
         parity["2"] = parity_decode(decode_layers, q.cpu().numpy(), decode_outs, threads)
     if not args.no_cpu:
-        step_s, reps, times = cpu_baseline_decode(kv, q.cpu().numpy(), threads, layers=decode_layers)
-        cpu_gbs = bytes_step / step_s / 1e9
-        out["cpu_baseline"] = {"value": round(cpu_gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+        # the box's CPU share, and wick's default pool, which clamps at 8 threads
+        # (src/engine.rs:53-56); the faster is the baseline, the other is kept beside it
+        runs = {}
+        for n in sorted({threads, 8}, reverse=True):
+            step_s, reps, times = cpu_baseline_decode(kv, q.cpu().numpy(), n, layers=decode_layers)
+            runs[n] = {"value": round(bytes_step / step_s / 1e9, 2), "unit": "GB/s", "ms_per_step": round(step_s * 1e3, 2),
+                       "reps": reps, "ms_per_step_min_max": [round(min(times) * 1e3, 2), round(max(times) * 1e3, 2)]}
+        best = min(runs, key=lambda n: runs[n]["ms_per_step"])
+        r = runs[best]
+        out["cpu_baseline"] = {"value": r["value"], "unit": "GB/s", "cores": best, "kind": "port",
                                "sample": f"wick's CPU attention restated in C (AVX2 order), all 24 decode layers at "
-                                         f"L=32768 on the host, median of {reps} full steps "
-                                         f"({step_s * 1e3:.1f} ms/step; {c['heads']} (token, head) items per layer "
-                                         f"over a {threads}-thread pool)",
-                               "ms_per_step": round(step_s * 1e3, 2),
-                               "ms_per_step_min_max": [round(min(times) * 1e3, 2), round(max(times) * 1e3, 2)],
-                               "host_cpu": cpu}
-        if threads != 8:
-            # wick's default pool clamps at 8 threads (src/engine.rs:53-56)
-            step8, reps8, times8 = cpu_baseline_decode(kv, q.cpu().numpy(), 8, layers=decode_layers)
-            out["cpu_baseline"]["threads_8"] = {"value": round(bytes_step / step8 / 1e9, 2), "unit": "GB/s",
-                                                "ms_per_step": round(step8 * 1e3, 2), "reps": reps8,
-                                                "ms_per_step_min_max": [round(min(times8) * 1e3, 2),
-                                                                        round(max(times8) * 1e3, 2)]}
+                                         f"L=32768 on the host, median of {r['reps']} full steps "
+                                         f"({r['ms_per_step']:.1f} ms/step; {c['heads']} (token, head) items per layer "
+                                         f"over a {best}-thread pool, the faster of {sorted(runs)} threads)",
+                               "ms_per_step": r["ms_per_step"], "ms_per_step_min_max": r["ms_per_step_min_max"],
+                               "host_cpu": cpu,
+                               "by_threads": {str(n): runs[n] for n in sorted(runs)}}
     del decode_layers
     if check:
         out["parity"] = {k: parity[k] for k in sorted(parity)}
