@@ -81,7 +81,7 @@ def test_qwen3_shape_qk_norm_prefill_then_decode():
 
 
 def test_decode_prep_with_split_chunks():
-    # len > 192: the decode splits into chunks; only the last chunk's workgroups append
+    # len > 192: the decode splits into contiguous chunks; only the last chunk's workgroups append
     run_chunks(14, 2, 64, [700, 1, 1], 1e6, bias=True, norm=True)
 
 
