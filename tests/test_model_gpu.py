@@ -302,6 +302,42 @@ def test_fixed_decode_chunk_past_the_fused_limit(chunk):
         assert m.decode(c2, first, 39) == ids[1:]
 
 
+def test_decode_loop_on_interleaved_splits():
+    """One-token forwards over 1200..1240 positions at head_dim 128 (group 4) with
+    512-key decode chunks: 3 workgroups per kv head whose waves each take at least
+    4 full rounds of 16-key groups, so the split deals the groups round-robin and
+    the new key's k/v rows are appended by whichever chunk holds them.  Logits
+    within 1e-4 of the CPU oracle and the same greedy ids through forward() and
+    through decode(), which replays captured steps reading the length on the
+    device."""
+    cfg = Config("qwen3", 256, 384, 2, 8, 2, 128, 300, rms_eps=1e-6, rope_theta=1e6, attn_bias=True, qk_norm=True)
+    w = _bias_and_norms(cfg, random_weights(cfg, seed=61, std=0.05), 62)
+    prompt = [int(x) for x in random_prompt(64, 1200, cfg.vocab)]
+    om = ol.OracleModel(cfg, w)
+    ost = om.new_state(1280)
+    want = om.forward(ost, prompt)
+    ids = []
+    with DeviceModel(cfg, w) as m:
+        cache = m.new_cache(1280)
+        cache.set_option(_native.OPT_DECODE_CHUNK, 512)
+        got = m.forward(cache, prompt)
+        for step in range(40):
+            L = len(prompt) + step + 1
+            assert -(-L // 16) >= 4 * -(-L // 512) * 4, "plan does not interleave"
+            diff = np.abs(got[-1] - want[-1]).max()
+            assert diff < 1e-4, f"step {step}: logits differ by {diff}"
+            tok = ol.argmax(want[-1])
+            assert int(np.argmax(got[-1])) == tok, f"step {step}"
+            ids.append(tok)
+            got = m.forward(cache, [tok])
+            want = om.forward(ost, [tok])
+        c2 = m.new_cache(1280)
+        c2.set_option(_native.OPT_DECODE_CHUNK, 512)
+        first = m.prefill(c2, prompt)
+        assert first == ids[0]
+        assert m.decode(c2, first, 39) == ids[1:]
+
+
 @pytest.mark.parametrize("shape", ["kv8-d32", "hidden2304-d64", "kv6-d128-bias-qknorm"])
 def test_unfused_single_token_paths(shape):
     """One-token forwards whose attention cannot carry the output projection --
