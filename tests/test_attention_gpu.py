@@ -105,11 +105,12 @@ def test_decode_chunk_option_values():
             kv.set_option(_native.OPT_DECODE_ORDER, good)
 
 
-# The interleaved split order applies when the kv head's key groups (16 keys at
-# head_dim 128, 32 at 64) give each of the nchunks x 4 waves at least 4 full rounds.
-def interleaved(L, d, nchunks):
+# The automatic key order interleaves a split on the MFMA core (head_dim 128, or
+# 64 with more than 4 heads per kv head) whose chunks hold at least 4 rounds of
+# the 4 waves' key groups (16 keys at head_dim 128, 32 at 64).
+def interleaves(d, chunk):
     gk = 16 if d == 128 else 32
-    return (L + gk - 1) // gk >= 4 * nchunks * 4
+    return chunk >= 4 * 4 * gk
 
 
 @pytest.mark.parametrize("d,heads,kv_heads,chunk,L", [
@@ -123,8 +124,7 @@ def test_decode_key_orders(d, heads, kv_heads, chunk, L):
     """Both split-K key orders against the oracle, on plans where the automatic
     order interleaves key groups across a kv head's workgroups (every unit
     starting its rounds at a different one), and bit-stable from call to call."""
-    nchunks = -(-L // chunk)
-    assert interleaved(L, d, nchunks)
+    assert interleaves(d, chunk) and L > chunk
     q, k, v = make_inputs(L + d, 1, L - 1, heads, kv_heads, d)
     want = ol.attention(q, k, v, 1, L - 1, heads, kv_heads, d)
     outs = {}

@@ -304,9 +304,9 @@ def test_fixed_decode_chunk_past_the_fused_limit(chunk):
 
 def test_decode_loop_on_interleaved_splits():
     """One-token forwards over 1200..1240 positions at head_dim 128 (group 4) with
-    512-key decode chunks: 3 workgroups per kv head whose waves each take at least
-    4 full rounds of 16-key groups, so the split deals the groups round-robin and
-    the new key's k/v rows are appended by whichever chunk holds them.  Logits
+    512-key decode chunks (8 rounds of the 4 waves' 16-key groups): 3 workgroups
+    per kv head, so the split deals the groups round-robin and the new key's k/v
+    rows are appended by whichever chunk holds them.  Logits
     within 1e-4 of the CPU oracle and the same greedy ids through forward() and
     through decode(), which replays captured steps reading the length on the
     device."""
@@ -322,8 +322,6 @@ def test_decode_loop_on_interleaved_splits():
         cache.set_option(_native.OPT_DECODE_CHUNK, 512)
         got = m.forward(cache, prompt)
         for step in range(40):
-            L = len(prompt) + step + 1
-            assert -(-L // 16) >= 4 * -(-L // 512) * 4, "plan does not interleave"
             diff = np.abs(got[-1] - want[-1]).max()
             assert diff < 1e-4, f"step {step}: logits differ by {diff}"
             tok = ol.argmax(want[-1])

@@ -111,7 +111,7 @@ def test_decode_prep_interleaved_new_key_not_in_last_chunk(heads, kv_heads, d, c
             start = base + s
             L = start + 1
             nchunks = -(-L // chunk)
-            assert -(-L // gk) >= 4 * nchunks * 4, "plan does not interleave"
+            assert chunk >= 4 * 4 * gk and nchunks > 1, "plan does not interleave"
             not_last.append((L - 1) // (4 * gk) % nchunks != nchunks - 1)
             q, k, v, _, _ = raw_inputs(base + 100 + s, 1, heads, kv_heads, d)
             att = kv.attend(0, heads, q, k, v, start)

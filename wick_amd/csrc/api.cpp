@@ -215,7 +215,7 @@ int plan_decode(wick_hip_kv *kv, int layer, int group, int len, const float *q_d
     a->chunk = chunk;
     a->nchunks = nchunks;
     a->stagger = nchunks > 1 && (long long)units * nchunks >= 2LL * kv->num_cus ? 1 : 0;
-    a->interleave = kv->decode_interleave;
+    a->interleave = kv->decode_interleave && wick::decode_interleaves(kv->head_dim, group, nchunks, chunk) ? 1 : 0;
     kv->last_grid = units * nchunks;
     return WICK_HIP_OK;
 }

@@ -874,11 +874,14 @@ struct DecodeSpace {
 // run on the VALU core (valu_core) instead of the MFMA tiles.
 // RP (PREP, NC > 0): the preparation is wave-local (WavePrep) instead of one
 // shared LDS copy behind a workgroup barrier.
+// ILV (NC == 0, 4 waves, several chunks): the interleaved key order
+// (DecodeArgs::interleave, KeyWalk).
 template <int D, bool PREP, bool PP = (D < 128), int NW = 4, int TG = Shape<D>::TG, bool OPROJ = false, int NC = 0,
-          bool RP = false>
+          bool RP = false, bool ILV = false>
 __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
     using S = Shape<D>;
     static_assert(NC == 0 || (D == 64 && NC <= 4), "the VALU core is for head_dim 64 and at most 4 heads");
+    static_assert(!ILV || (NC == 0 && D >= 64 && !OPROJ), "the interleaved order is the lean MFMA core's");
     static_assert(!RP || (PREP && NC > 0), "wave-local preparation is the VALU core's");
     __shared__ float sm_m[NW][16], sm_l[NW][16];
     __shared__ __attribute__((aligned(16))) float sm_o[NW][16][D];
@@ -897,19 +900,11 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
     const float *Vh = a.v + (size_t)kvh * a.capacity * D;
     // the cache length: the argument, or (graph-replayed decode loop) a device counter
     const int len = a.len_dev ? *a.len_dev : a.len;
-    // Interleaved split (DecodeArgs::interleave; KeyWalk): at any moment the
-    // workgroups of a kv head read one window of its cache rather than
-    // nchunks streams a chunk apart.  It pays from kDecodeInterleaveRounds
-    // full rounds of groups per wave (Llama-3-8B shape: 65536 positions
-    // 84.8 -> 83.2 us, 32768 47.6 -> 46.7 us) and loses below (16384: 27.4
-    // -> 28.3-29.3 us, 8192: 17.1 -> 17.5 us).  owner: the chunk that holds
-    // position len-1.
-    constexpr int GKc = 16 * TG;
-    const bool ilv = NC == 0 && D >= 64 && !OPROJ && a.interleave && a.nchunks > 1 &&
-                     (len + GKc - 1) / GKc >= kDecodeInterleaveRounds * a.nchunks * NW;
-    const int kbeg = ilv ? chunk * NW * GKc : chunk * a.chunk;
-    const int kend = ilv ? len : min(kbeg + a.chunk, len);
-    const int owner = ilv ? (len - 1) / (NW * GKc) % a.nchunks : a.nchunks - 1;
+    // ILV (DecodeArgs::interleave): the wave's key groups are dealt
+    // round-robin over the kv head's chunks (KeyWalk) instead of one
+    // contiguous range per chunk.  owner: the chunk that holds position len-1.
+    const int kbeg = ILV ? 0 : chunk * a.chunk, kend = ILV ? len : min(kbeg + a.chunk, len);
+    const int owner = ILV ? (len - 1) / (NW * 16 * TG) % a.nchunks : a.nchunks - 1;
 
     // OPROJ: this wave's kOprojRows rows of wo over the unit's ncols*D
     // columns, requested before anything waits on memory: lane l holds column
@@ -1018,11 +1013,10 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
         for (int db = 0; db < S::DB; db++) st.o[db] = f4{0.f, 0.f, 0.f, 0.f};
         constexpr int GK = 16 * TG;                 // keys per group
         constexpr bool kStreamV = D == 128 || PP;  // V through the streaming policy (lean_load_global_v)
-        const KeyWalk walk = ilv ? KeyWalk::interleaved(len, a.nchunks, chunk, NW, w, GK, unit)
-                                 : KeyWalk::contiguous(kbeg + GK * w, kend, NW * GK);
-        const int n = walk.n;
-        if constexpr (PP) {
-            // the next group's loads go out before this group's products
+        if constexpr (ILV && PP) {
+            // the contiguous loops below over the walk's positions
+            const KeyWalk walk = KeyWalk::interleaved(len, a.nchunks, chunk, NW, w, GK, unit);
+            const int n = walk.n;
             LeanGroup<D, TG> ta, tb;
             int p0 = walk.p;
             if (n > 0) lean_load_global<D, TG, kStreamV>(Kh, Vh, p0, kend, p0 + GK > kend, lane, ta);
@@ -1038,9 +1032,49 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
                 lean_step<D, false, TG>(tb, q, p1, p1 + GK > kend, kend, g, st.m, st.l, st.o);
                 p0 = p2;
             }
-        } else {
+        } else if constexpr (ILV) {
+            const KeyWalk walk = KeyWalk::interleaved(len, a.nchunks, chunk, NW, w, GK, unit);
+            const int n = walk.n;
             int p0 = walk.p, j = 0;
             if (n > 0) {
+                LeanGroup<D, TG> t;
+                const bool tail = p0 + GK > kend;
+                lean_load_global_k<D, TG>(Kh, p0, kend, tail, lane, t);
+                __builtin_amdgcn_sched_barrier(0);
+                scale_q();
+                if (a.stagger) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                lean_load_global_v<D, TG, kStreamV>(Vh, p0, kend, tail, lane, t);
+                lean_step<D, false, TG>(t, q, p0, tail, kend, g, st.m, st.l, st.o);
+                p0 = walk.next(p0, j++);
+            }
+            for (; j < n; p0 = walk.next(p0, j++)) {
+                LeanGroup<D, TG> t;
+                const bool tail = p0 + GK > kend;
+                lean_load_global<D, TG, kStreamV>(Kh, Vh, p0, kend, tail, lane, t);
+                lean_step<D, false, TG>(t, q, p0, tail, kend, g, st.m, st.l, st.o);
+            }
+        } else if constexpr (PP) {
+            const int wbeg = __builtin_amdgcn_readfirstlane(kbeg + GK * w), step = NW * GK;
+            // the next group's loads go out before this group's products
+            LeanGroup<D, TG> ta, tb;
+            int p0 = wbeg;
+            if (p0 < kend) lean_load_global<D, TG, kStreamV>(Kh, Vh, p0, kend, p0 + GK > kend, lane, ta);
+            __builtin_amdgcn_sched_barrier(0);
+            scale_q();
+            while (p0 < kend) {
+                const int p1 = p0 + step;
+                if (p1 < kend) lean_load_global<D, TG, kStreamV>(Kh, Vh, p1, kend, p1 + GK > kend, lane, tb);
+                lean_step<D, false, TG>(ta, q, p0, p0 + GK > kend, kend, g, st.m, st.l, st.o);
+                if (p1 >= kend) break;
+                const int p2 = p1 + step;
+                if (p2 < kend) lean_load_global<D, TG, kStreamV>(Kh, Vh, p2, kend, p2 + GK > kend, lane, ta);
+                lean_step<D, false, TG>(tb, q, p1, p1 + GK > kend, kend, g, st.m, st.l, st.o);
+                p0 = p2;
+            }
+        } else {
+            const int wbeg = __builtin_amdgcn_readfirstlane(kbeg + GK * w), step = NW * GK;
+            int p0 = wbeg;
+            if (p0 < kend) {
                 LeanGroup<D, TG> t;
                 const bool tail = p0 + GK > kend;
                 lean_load_global_k<D, TG>(Kh, p0, kend, tail, lane, t);
@@ -1054,9 +1088,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
                 if (a.stagger) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 lean_load_global_v<D, TG, kStreamV>(Vh, p0, kend, tail, lane, t);
                 lean_step<D, false, TG>(t, q, p0, tail, kend, g, st.m, st.l, st.o);
-                p0 = walk.next(p0, j++);
+                p0 += step;
             }
-            for (; j < n; p0 = walk.next(p0, j++)) {
+            for (; p0 < kend; p0 += step) {
                 LeanGroup<D, TG> t;
                 const bool tail = p0 + GK > kend;
                 lean_load_global<D, TG, kStreamV>(Kh, Vh, p0, kend, tail, lane, t);
@@ -1599,6 +1633,12 @@ void launch_decode_core(const DecodeArgs &a, dim3 grid, hipStream_t s) {
         default: break;
         }
     }
+    if constexpr (D >= 64 && NW == 4 && !OPROJ) {
+        if (a.interleave) {
+            hipLaunchKernelGGL((decode_kernel<D, PREP, PP, NW, TG, OPROJ, 0, false, true>), grid, block, 0, s, a);
+            return;
+        }
+    }
     hipLaunchKernelGGL((decode_kernel<D, PREP, PP, NW, TG, OPROJ, 0>), grid, block, 0, s, a);
 }
 
@@ -1668,6 +1708,16 @@ hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+bool decode_interleaves(int head_dim, int group, int nchunks, int chunk) {
+    // the lean MFMA core's 4-wave split (not the VALU core of head_dim 64 with
+    // at most 4 heads per unit), with chunks of at least kDecodeInterleaveRounds
+    // rounds of the 4 waves' key groups: every chunk's wave 0 then has a group
+    // (len > (nchunks - 1) * chunk), and each wave about that many full rounds
+    if (nchunks < 2 || (head_dim != 64 && head_dim != 128) || (head_dim == 64 && group <= 4)) return false;
+    const int gk = 16 * (head_dim == 128 ? Shape<128>::TG : Shape<64>::TG);  // keys per group
+    return chunk >= kDecodeInterleaveRounds * 4 * gk;
 }
 
 bool decode_oproj_supported(int head_dim, int group, int nchunks, int chunk) {

@@ -27,12 +27,10 @@ struct DecodeArgs {
     // a grid of at least two workgroups per CU, streaming from HBM: each wave
     // requests its first group's V rows only once its K rows have arrived
     int stagger;
-    // Key order of a split (several chunks, head_dim 64 / 128 on the MFMA
-    // tiles): 0 = chunk c takes positions c*chunk .. +chunk; 1 = interleaved
-    // where the length the kernel reads gives every wave at least
-    // kDecodeInterleaveRounds full rounds: wave w of chunk c takes the key
-    // groups (i*nchunks + c)*waves + w of the whole context (rounds i rotated
-    // per unit), contiguous chunks otherwise.
+    // Key order of a split: 0 = chunk c takes positions c*chunk .. +chunk;
+    // 1 (only where decode_interleaves holds) = wave w of chunk c takes the
+    // key groups (i*nchunks + c)*waves + w of the whole context, i = 0, 1, ...
+    // (the full rounds i rotated per unit).
     int interleave;
     float scale;
     // Fused input preparation (prep != 0): q is raw; kraw / vraw [kv_heads*D]
@@ -64,7 +62,8 @@ constexpr int kOprojChunks = 4;
 // Longest chunk the fused form takes (8 waves x one 32-key group each).
 constexpr int kOprojMaxChunk = 8 * 2 * 16;
 
-// Fewest full rounds of key groups per wave for the interleaved split order.
+// Fewest rounds of key groups per wave (chunk / (4 waves x keys per group))
+// for the interleaved split order.
 constexpr int kDecodeInterleaveRounds = 4;
 
 struct PrefillArgs {
@@ -120,6 +119,8 @@ hipError_t launch_decode(int head_dim, const DecodeArgs &a, int grid, hipStream_
 // 64 or 128, one chunk of at most kOprojMaxChunk keys per unit, the unit's
 // columns fit kOprojChunks).
 bool decode_oproj_supported(int head_dim, int group, int nchunks, int chunk);
+// Whether a split plan takes the interleaved key order (DecodeArgs::interleave).
+bool decode_interleaves(int head_dim, int group, int nchunks, int chunk);
 // The fused decode + partial output projection (a.prep set, a.nchunks == 1):
 // units x ceil(hidden / (8 kOprojRows)) workgroups of 8 waves.
 hipError_t launch_decode_oproj(int head_dim, DecodeArgs a, hipStream_t s);
