@@ -208,11 +208,11 @@ COPY_MIB = 256
 
 def decode_kernel_label(nchunks):
     """The kernels of one configs[1] decode call as rocprofv3 names them: the split
-    kernel's single-buffered 4-wave instance (every wave takes one group of tiles
-    at 128-key chunks) and the merge instance whose 16 x NB child slots cover
-    nchunks."""
+    kernel's single-buffered 4-wave instance in the contiguous key order (every
+    wave takes one group of tiles at 128-key chunks) and the merge instance whose
+    16 x NB child slots cover nchunks."""
     nb = next(n for n in (1, 2, 4, 8, 16) if 16 * n >= nchunks)
-    return (f"wick::decode_kernel<64, false, false, 4, 2, false, 0, false> + wick::decode_merge_kernel<64, {nb}> "
+    return (f"wick::decode_kernel<64, false, false, 4, 2, false, 0, false, false> + wick::decode_merge_kernel<64, {nb}> "
             f"(one call, {nchunks} chunks per kv head)")
 
 
