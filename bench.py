@@ -327,24 +327,23 @@ def parity_attention(q, k, v, t, start, heads, kv_heads, d, att, threads):
     return tol_record(att, want)
 
 
-def cpu_baseline_decode(kv, q_host, threads, budget_s=12.0, max_reps=7, layers=None):
-    """wick's CPU attention (the oracle) on the host: decode over all 24 layers, median of reps."""
-    import numpy as np
+def cpu_baseline_decode(q_host, thread_counts, layers, budget_s=24.0, max_reps=7):
+    """wick's CPU attention (the oracle) on the host: decode over all 24 layers, one
+    full step per pool size in turn (so that a slow spell of the host does not fall
+    on one pool size only), up to max_reps rounds; {threads: step times}."""
     ol = oracle_lib()
     c = DEC
-    if layers is None:
-        layers = read_decode_layers(kv)
-    times = []
+    times = {n: [] for n in thread_counts}
     t_start = time.perf_counter()
-    while len(times) < max_reps and (time.perf_counter() - t_start) < budget_s:
-        t0 = time.perf_counter()
-        for layer in range(c["layers"]):
-            k, v = layers[layer]
-            ol.attention(q_host[layer:layer + 1], k, v, 1, c["L"] - 1, c["heads"], c["kv_heads"], c["d"],
-                         threads=threads)
-        times.append(time.perf_counter() - t0)
-    step_s = float(np.median(times))
-    return step_s, len(times), times
+    while len(times[thread_counts[-1]]) < max_reps and (time.perf_counter() - t_start) < budget_s:
+        for n in thread_counts:
+            t0 = time.perf_counter()
+            for layer in range(c["layers"]):
+                k, v = layers[layer]
+                ol.attention(q_host[layer:layer + 1], k, v, 1, c["L"] - 1, c["heads"], c["kv_heads"], c["d"],
+                             threads=n)
+            times[n].append(time.perf_counter() - t0)
+    return times
 
 
 def read_decode_layers(kv):
@@ -965,16 +964,17 @@ def main():
     if not args.no_cpu:
         # the box's CPU share, and wick's default pool, which clamps at 8 threads
         # (src/engine.rs:53-56); the faster is the baseline, the other is kept beside it
+        import numpy as np
         runs = {}
-        for n in sorted({threads, 8}, reverse=True):
-            step_s, reps, times = cpu_baseline_decode(kv, q.cpu().numpy(), n, layers=decode_layers)
+        for n, times in cpu_baseline_decode(q.cpu().numpy(), sorted({threads, 8}, reverse=True), decode_layers).items():
+            step_s = float(np.median(times))
             runs[n] = {"value": round(bytes_step / step_s / 1e9, 2), "unit": "GB/s", "ms_per_step": round(step_s * 1e3, 2),
-                       "reps": reps, "ms_per_step_min_max": [round(min(times) * 1e3, 2), round(max(times) * 1e3, 2)]}
+                       "reps": len(times), "ms_per_step_min_max": [round(min(times) * 1e3, 2), round(max(times) * 1e3, 2)]}
         best = min(runs, key=lambda n: runs[n]["ms_per_step"])
         r = runs[best]
         out["cpu_baseline"] = {"value": r["value"], "unit": "GB/s", "cores": best, "kind": "port",
                                "sample": f"wick's CPU attention restated in C (AVX2 order), all 24 decode layers at "
-                                         f"L=32768 on the host, median of {r['reps']} full steps "
+                                         f"L=32768 on the host, median of {r['reps']} full steps, alternating pool sizes "
                                          f"({r['ms_per_step']:.1f} ms/step; {c['heads']} (token, head) items per layer "
                                          f"over a {best}-thread pool, the faster of {sorted(runs)} threads)",
                                "ms_per_step": r["ms_per_step"], "ms_per_step_min_max": r["ms_per_step_min_max"],
