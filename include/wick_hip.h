@@ -139,7 +139,11 @@ int wick_hip_kv_synchronize(wick_hip_kv *kv);
 
 /* Tuning knobs. */
 #define WICK_HIP_OPT_DECODE_CHUNK 1 /* positions per decode workgroup (a multiple of 16, at least 64; 0 = automatic) */
-#define WICK_HIP_OPT_DECODE_ORDER 2 /* split-K key order: 1 = automatic (interleaved on long contexts; default), 0 = contiguous chunks */
+/* Split-K key order: 1 = automatic (the default: chunks of at least 256 keys at
+ * head_dim 128, or 512 at head_dim 64 with more than 4 query heads per kv head,
+ * are read as key groups dealt round-robin over the kv head's workgroups),
+ * 0 = one contiguous chunk per workgroup. */
+#define WICK_HIP_OPT_DECODE_ORDER 2
 int wick_hip_kv_set_option(wick_hip_kv *kv, int option, int value);
 
 /* Number of workgroups the last attention call launched (for measurement). */

@@ -781,30 +781,17 @@ __device__ __forceinline__ void valu_core(const float *__restrict__ Kh, const fl
 
 // ------------------------------------------------------------------ decode
 
-// The key groups one wave of a split decode takes, in order: n groups of gk
-// keys, the first at position p; next(p, j) gives the position of group j + 1
-// from group j's.  All fields are wave-uniform.
-//   contiguous: positions p, p + step, ... below the chunk's end.
-//   interleaved: the kv head's groups dealt round-robin to the waves of its
-//     nchunks workgroups (slot = chunk * waves + wave): F full rounds of
-//     `slots` groups, then one partial round.  Unit u starts its full rounds
-//     at round u mod F, so the kv heads (each on its own XCD when there are
-//     8 units) do not read the same offsets of their caches at the same time
-//     (without the rotation the Llama-3-8B shape at 32768 positions ran
-//     48.6-48.8 us against 46.7-46.8).
+// The key groups one wave of an interleaved split decode takes, in order: n
+// groups of gk keys, the first at position p; next(p, j) gives the position of
+// group j + 1 from group j's.  All fields are wave-uniform.  The kv head's
+// groups are dealt round-robin to the waves of its nchunks workgroups (slot =
+// chunk * waves + wave): F full rounds of `slots` groups, then one partial
+// round.  Unit u starts its full rounds at round u mod F, so the kv heads (each
+// on its own XCD when there are 8 units) do not read the same offsets of their
+// caches at the same time (without the rotation the Llama-3-8B shape at 32768
+// positions ran 48.6-48.8 us against 46.7-46.8).
 struct KeyWalk {
     int p, n, step, wrap, full, tailp;
-
-    __device__ static KeyWalk contiguous(int p0, int end, int step) {
-        KeyWalk k;
-        k.p = __builtin_amdgcn_readfirstlane(p0);
-        k.n = __builtin_amdgcn_readfirstlane(p0 < end ? (end - p0 + step - 1) / step : 0);
-        k.step = step;
-        k.wrap = 0x7fffffff;
-        k.full = -1;
-        k.tailp = 0;
-        return k;
-    }
 
     __device__ static KeyWalk interleaved(int len, int nchunks, int chunk, int waves, int w, int gk, int unit) {
         const int slots = nchunks * waves, ngroups = (len + gk - 1) / gk;
@@ -903,7 +890,8 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
     // ILV (DecodeArgs::interleave): the wave's key groups are dealt
     // round-robin over the kv head's chunks (KeyWalk) instead of one
     // contiguous range per chunk.  owner: the chunk that holds position len-1.
-    const int kbeg = ILV ? 0 : chunk * a.chunk, kend = ILV ? len : min(kbeg + a.chunk, len);
+    const int kbeg = ILV ? 0 : chunk * a.chunk;  // (unused by ILV)
+    const int kend = ILV ? len : min(kbeg + a.chunk, len);
     const int owner = ILV ? (len - 1) / (NW * 16 * TG) % a.nchunks : a.nchunks - 1;
 
     // OPROJ: this wave's kOprojRows rows of wo over the unit's ncols*D
