@@ -85,12 +85,14 @@ def test_decode_prep_with_split_chunks():
     run_chunks(14, 2, 64, [700, 1, 1], 1e6, bias=True, norm=True)
 
 
-@pytest.mark.parametrize("heads,kv_heads,d,chunk,base", [(32, 8, 128, 512, 1918), (14, 2, 64, 1024, 2900)])
+@pytest.mark.parametrize("heads,kv_heads,d,chunk,base", [(32, 8, 128, 512, 1918), (14, 2, 64, 1024, 2900),
+                                                        (40, 2, 64, 1024, 2900)])
 def test_decode_prep_interleaved_new_key_not_in_last_chunk(heads, kv_heads, d, chunk, base):
     """Single-token steps with the preparation in the decode kernel's prologue,
     on plans that interleave key groups across a kv head's workgroups: the new
     position's k and v rows are prepared and appended by the workgroups whose
-    groups hold it, which here are not the last chunk's."""
+    groups hold it, which here are not the last chunk's (with 40 heads per 2 kv
+    heads, by both 16-head slices of the kv head, which write the same bits)."""
     gk = 16 if d == 128 else 32
     inv = ol.rope_inv_freq(1e6, d)
     rng = np.random.default_rng(base)
