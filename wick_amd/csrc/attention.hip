@@ -612,9 +612,9 @@ __device__ __forceinline__ void lean_step(const LeanGroup<D, TG> &t, const f4 (&
 // ------------------------------------------------------------------ VALU decode core
 //
 // For a decode unit of NC <= 4 query heads (GQA groups of at most 4) the
-// 16-column MFMA tiles leave at least 12 of their 16 columns idle, and
-// gfx950's VALU FMAs run at the same f32 rate as its MFMAs, so this core runs
-// the products on the VALU (head_dim 64).  A wave steps over groups of 32
+// 16-column MFMA tiles leave at least 12 of their 16 columns idle, while
+// gfx950's (unpacked) f32 VALU FMAs run at half the f32 MFMA rate, so this
+// core runs the products on the VALU (head_dim 64).  A wave steps over groups of 32
 // keys:
 //   QK: lane (key kl = l/2, half hh = l%2) holds float4s 2j + hh (j < 8) of
 //       its key's K row and of each head's q row: 8 dot4s per head, then the
@@ -837,8 +837,9 @@ struct DecodeSpace {
 };
 
 // One token (t = 1) over len cached positions, split-K: workgroup
-// (unit, chunk) runs 4 waves over positions chunk*C .. +C of one kv head for
-// up to 16 of its query heads (unit = kv head x 16-head slice), so every K/V
+// (unit, chunk) runs 4 waves over positions chunk*C .. +C of one kv head (or,
+// with ILV, over its share of the kv head's key groups) for up to 16 of its
+// query heads (unit = kv head x 16-head slice), so every K/V
 // byte is read once for the whole GQA group.  With one chunk the output is
 // written directly; otherwise the chunk's (max, sum, O) state per query head
 // goes to the workspace and decode_merge_kernel, the next launch on the
