@@ -498,7 +498,8 @@ def measure_long_decode(torch, kv_cls, native, dev, steps, ceiling=True, check_t
     torch.cuda.empty_cache()
     best = sweep[0]
     out = {"workload": "Llama-3-8B shape (Hq 32 / Hkv 8, d 128), 32 layers x 65536 positions (16 GiB K+V), "
-                       "one query token per layer per step, eager launches",
+                       "one query token per layer per step, eager launches; split-K key order automatic "
+                       "(chunks of >= 256 keys read as interleaved 16-key groups)",
            "bytes_per_layer": bytes_layer, "auto": best, "chunk_sweep": sweep, "at_32k_context": at32,
            "steps_64": steps64, "parity": parity}
     if ceiling:
