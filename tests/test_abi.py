@@ -28,6 +28,16 @@ def test_header_and_binding_agree():
     assert header_symbols() == set(_native.SIGNATURES)
 
 
+def test_header_constants_and_binding_agree():
+    """Status codes and option numbers: the header's #defines and the Python binding's."""
+    with open(os.path.join(ROOT, "include", "wick_hip.h")) as f:
+        defs = dict(re.findall(r"#define WICK_HIP_(\w+)\s+\(?(-?\d+)\)?", f.read()))
+    assert {k: int(v) for k, v in defs.items()} == {
+        "OK": _native.OK, "EINVAL": _native.EINVAL, "EHIP": _native.EHIP, "ENOMEM": _native.ENOMEM,
+        "EDEVICE": _native.EDEVICE, "OPT_DECODE_CHUNK": _native.OPT_DECODE_CHUNK,
+        "OPT_DECODE_ORDER": _native.OPT_DECODE_ORDER}
+
+
 def test_library_exports_every_symbol():
     lib = _native.load()
     for name in header_symbols():
