@@ -327,10 +327,11 @@ def parity_attention(q, k, v, t, start, heads, kv_heads, d, att, threads):
     return tol_record(att, want)
 
 
-def cpu_baseline_decode(q_host, thread_counts, layers, budget_s=24.0, max_reps=7):
+def cpu_baseline_decode(q_host, thread_counts, layers, budget_s=20.0, max_reps=40):
     """wick's CPU attention (the oracle) on the host: decode over all 24 layers, one
     full step per pool size in turn (so that a slow spell of the host does not fall
-    on one pool size only), up to max_reps rounds; {threads: step times}."""
+    on one pool size only), up to max_reps rounds or budget_s seconds of CPU work
+    (at least one round); {threads: step times}."""
     ol = oracle_lib()
     c = DEC
     times = {n: [] for n in thread_counts}
