@@ -609,6 +609,112 @@ __device__ __forceinline__ void lean_step(const LeanGroup<D, TG> &t, const f4 (&
     if constexpr (LAZY) __builtin_amdgcn_s_setprio(0);
 }
 
+// The two-block prefill step at head_dim 128 (lean2), software-pipelined in
+// the instruction stream: block A's QK products; then block B's QK products
+// with A's masking and column max placed one VALU instruction between each
+// two products; A's rescale (rare), weights and PV products; B's masking and
+// column max between A's PV products; B's rescale, weights and PV products.
+// The arithmetic is lean_step's (LAZY); only the order of independent
+// instructions changes (config 3 T=2048: 172.2-173.4 -> 165.3-165.6 us).
+template <int D, int TG>
+__device__ __forceinline__ void lean_qk(const LeanGroup<D, TG> &t, const f4 (&q)[Shape<D>::KJ], float (&sc)[TG][4]) {
+    using S = Shape<D>;
+#pragma unroll
+    for (int u = 0; u < TG; u++) {
+        f4 sacc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < S::KJ; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) sacc = mfma16x16x4(t.k[u][j][e], q[j][e], sacc);
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) sc[u][rr] = sacc[rr];
+    }
+}
+
+// masking (a select, not a branch, so the step stays one scheduling region)
+// and the column max of the scores
+template <int TG>
+__device__ __forceinline__ void lean_mask_max(float (&sc)[TG][4], int p0, int klimit, int g, float &cm) {
+#pragma unroll
+    for (int u = 0; u < TG; u++)
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) sc[u][rr] = (p0 + 16 * u + 4 * g + rr < klimit) ? sc[u][rr] : -INFINITY;
+    float lm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < TG; u++) lm = smax(lm, smax(smax(sc[u][0], sc[u][1]), smax(sc[u][2], sc[u][3])));
+    cm = col_max(lm);
+}
+
+// the lazy reference max (rescale when a column passes m by kLazyMax), then
+// the weights 2^(s - m) and their sum
+template <int D, int TG>
+__device__ __forceinline__ void lean_weights(const float (&sc)[TG][4], float cm, float &m, float &l,
+                                             f4 (&o)[Shape<D>::DB], float (&e)[TG][4]) {
+    using S = Shape<D>;
+    const bool grow = cm > m + kLazyMax;  // never for cm = -inf
+    if (__any(grow)) {
+        const float alpha = grow ? exp2_fast(m - cm) : 1.0f;  // 0 from the floor
+        l *= alpha;
+#pragma unroll
+        for (int db = 0; db < S::DB; db++) o[db] *= alpha;
+        m = grow ? cm : m;
+    }
+    float ls = 0.f;
+#pragma unroll
+    for (int u = 0; u < TG; u++)
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+            e[u][rr] = exp2_fast(sc[u][rr] - m);
+            ls += e[u][rr];
+        }
+    l += ls;
+}
+
+template <int D, int TG>
+__device__ __forceinline__ void lean_pv(const LeanGroup<D, TG> &t, const float (&e)[TG][4], f4 (&o)[Shape<D>::DB]) {
+    using S = Shape<D>;
+#pragma unroll
+    for (int u = 0; u < TG; u++)
+#pragma unroll
+        for (int mm = 0; mm < 4; mm++)
+#pragma unroll
+            for (int db = 0; db < S::DB; db++) o[db] = mfma16x16x4(t.v[u][mm][db / 4][db % 4], e[u][mm], o[db]);
+}
+
+// scheduling groups for the region before the next sched_barrier: N times one
+// MFMA then one VALU (transcendental included) instruction
+template <int N>
+__device__ __forceinline__ void interleave_mfma_valu() {
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x402, 1, 0);
+    }
+}
+
+template <int D, int TG>
+__device__ __forceinline__ void lean_step2(const LeanGroup<D, TG> &t, const f4 (&q)[2][Shape<D>::KJ], int p0,
+                                           const int (&klimit)[2], int g, float (&m)[2], float (&l)[2],
+                                           f4 (&o)[2][Shape<D>::DB]) {
+    float sa[TG][4], sb[TG][4], ea[TG][4], eb[TG][4], cma, cmb;
+    __builtin_amdgcn_s_setprio(1);
+    lean_qk<D, TG>(t, q[0], sa);
+    __builtin_amdgcn_sched_barrier(0);
+    lean_qk<D, TG>(t, q[1], sb);
+    lean_mask_max<TG>(sa, p0, klimit[0], g, cma);
+    interleave_mfma_valu<16>();
+    __builtin_amdgcn_sched_barrier(0);
+    lean_weights<D, TG>(sa, cma, m[0], l[0], o[0], ea);
+    __builtin_amdgcn_sched_barrier(0);
+    lean_pv<D, TG>(t, ea, o[0]);
+    lean_mask_max<TG>(sb, p0, klimit[1], g, cmb);
+    interleave_mfma_valu<16>();
+    __builtin_amdgcn_sched_barrier(0);
+    lean_weights<D, TG>(sb, cmb, m[1], l[1], o[1], eb);
+    lean_pv<D, TG>(t, eb, o[1]);
+    __builtin_amdgcn_s_setprio(0);
+}
+
 // ------------------------------------------------------------------ VALU decode core
 //
 // For a decode unit of NC <= 4 query heads (GQA groups of at most 4) the
@@ -1439,9 +1545,13 @@ __device__ __forceinline__ void prefill_lean_body(const PrefillArgs &a) {
         LeanGroup<D> t;
         lean_load<D>(rk, rv, vk, vv, p0, t);
         // keys past a row's causal limit or past the wave's range
+        if constexpr (RB == 2 && D == 128) {
+            lean_step2<D, TG>(t, q, p0, klimit, g, m, l, o);
+        } else {
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++)
-            lean_step<D, true>(t, q[rb], p0, p0 + 16 * TG > unmasked_end[rb], klimit[rb], g, m[rb], l[rb], o[rb]);
+            for (int rb = 0; rb < RB; rb++)
+                lean_step<D, true>(t, q[rb], p0, p0 + 16 * TG > unmasked_end[rb], klimit[rb], g, m[rb], l[rb], o[rb]);
+        }
     }
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
